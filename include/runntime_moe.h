@@ -1,0 +1,150 @@
+/* runntime_moe.h — C ABI of the MI355X int8 mixture-of-experts layer.
+ *
+ * The drop-in boundary for ruNNtime's `runntime/core` MoE ops. Every entry
+ * point replaces one reference interface (paths relative to
+ * packages/runntime/ in software-mansion/runntime):
+ *
+ *   moe_topk         topk(x, k)                    src/core/graph/ops/reduce.ts:93-100,
+ *                                                  kernel src/core/kernels/reduce/topkSelect.ts:21-92
+ *   moe_router_topk  topk(gate.forward(xn), k)     src/zoo/privacy-filter/moeMlp.ts:83 (router
+ *                                                  Linear, src/core/nn/layers.ts:252-263, fused with topk)
+ *   moe_up           moeUp(x, route, glu, lin, {bits, groupSize})
+ *                                                  src/core/graph/ops/matmul.ts:220-244,
+ *                                                  kernel src/core/kernels/matmul/moeQuantW.ts:122-175
+ *   moe_down         moeDown(act, route, out, residual, {bits, groupSize})
+ *                                                  src/core/graph/ops/matmul.ts:246-272,
+ *                                                  kernel src/core/kernels/matmul/moeQuantW.ts:188-237
+ *   moe_layer        the quantized branch of EagerMoeMlp.forward after rmsNorm:
+ *                    topk(router) → moeUp → moeDown  src/zoo/privacy-filter/moeMlp.ts:82-121
+ *   moe_ctx_* / moe_sync / moe_last_error
+ *                    the executor contract the ops run under: one queue per
+ *                    context, errors as codes (src/core/graph/evalCore.ts:14-31,
+ *                    src/core/error.ts:3-50)
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers (HBM), plain and unowned. The
+ *     caller keeps them alive until the work is done (moe_sync, or an event
+ *     on the stream given to moe_ctx_create).
+ *   - Layouts are the reference's (src/core/graph/ops/matmul.ts:212-218):
+ *       route    f32 [T, 2k]: k expert ids stored as exact floats, then k
+ *                gate weights (topkSelect.ts:13-18, :148-156)
+ *       w        quantW u32 words of the logical [E·K, N] int8/int4 weight:
+ *                16-value tiles per (expert, 4-column unit, 4-row chunk),
+ *                column-major in the tile (src/core/kernels/quantCommon.ts:8-15)
+ *       scales   f32 [E·K/groupSize, N]
+ *       bias     f32 [E, N] (may be NULL: zero)
+ *       act      f32 [T·k, N], row t·k + s
+ *   - The reference compiles in k = 4 (moeQuantW.ts:28); here k is a
+ *     parameter, 1 ≤ k ≤ 16, and k = 4 is the reference's case.
+ *   - Every call is asynchronous on the context's stream. Return value: 0 on
+ *     success, else an moe_status code with a message in moe_last_error().
+ */
+#ifndef RUNNTIME_MOE_H
+#define RUNNTIME_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef MOE_API
+#define MOE_API __attribute__((visibility("default")))
+#endif
+
+/* The reference's RunntimeError codes that this layer can raise
+ * (src/core/error.ts:3-21). */
+typedef enum moe_status {
+  MOE_OK = 0,
+  MOE_INVALID_ARGUMENT = 1, /* 'INVALID_ARGUMENT' */
+  MOE_EXECUTION_FAILED = 2, /* 'EXECUTION_FAILED' */
+  MOE_NOT_INITIALIZED = 3,  /* 'NOT_INITIALIZED'  */
+  MOE_RESOURCE_DISPOSED = 4 /* 'RESOURCE_DISPOSED' */
+} moe_status;
+
+/* Element type of a float input (the reference's 'f32' | 'f16' dtypes,
+ * src/core/graph/value.ts). */
+typedef enum moe_dtype { MOE_F32 = 0, MOE_F16 = 1 } moe_dtype;
+
+typedef struct moe_ctx moe_ctx;
+
+/* One routed layer's weights for all E experts — the reference's
+ * `interface QuantExpertWeight { w; scales; bias }`
+ * (src/core/graph/ops/matmul.ts:212-218). */
+typedef struct moe_expert_weight {
+  const uint32_t *w;    /* quantW words, E·K·N·bits/32 of them */
+  const float *scales;  /* [E·K/groupSize, N] */
+  const float *bias;    /* [E, N] or NULL */
+} moe_expert_weight;
+
+/* Library version, for the binding to check it loaded what it expects. */
+MOE_API int moe_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+MOE_API const char *moe_last_error(void);
+
+/* A context owns one HIP stream (or borrows `stream`, a hipStream_t, when it
+ * is not NULL) and the device workspace the layer needs between kernels.
+ * Replaces initRunntime(root)/gpuExecutor(root) (src/core/gpu/eval.ts:80-100). */
+MOE_API int moe_ctx_create(int device, void *stream, moe_ctx **out);
+/* Switch the stream later calls enqueue on (NULL: the context's own). */
+MOE_API int moe_ctx_set_stream(moe_ctx *ctx, void *stream);
+/* Grow the workspace now for layers up to these sizes, so later calls with
+ * no larger shapes allocate nothing. */
+MOE_API int moe_ctx_reserve(moe_ctx *ctx, int T, int d, int I, int E, int k);
+MOE_API int moe_ctx_destroy(moe_ctx *ctx);
+/* Wait for the context's stream; reports a device fault as EXECUTION_FAILED. */
+MOE_API int moe_sync(moe_ctx *ctx);
+
+/* topk(x, k): x [T, E] logits (f32 or f16) → route f32 [T, 2k]. Descending,
+ * lowest id on ties, softmax over the k picked logits; the reference's
+ * −3.4e38 start value is kept (a logit at or below it never enters). */
+MOE_API int moe_topk(moe_ctx *ctx, const void *logits, moe_dtype dtype, int T, int E, int k,
+             float *route);
+
+/* Router + topk fused: logits = x·W + b with W f32 [d, E] (the reference's
+ * Linear weight after its load-time transpose), summed in this library's
+ * canonical f32 order (64-wide fma chunks folded left to right, then + b),
+ * then topk as moe_topk. x is f32 or f16 [T, d]; b may be NULL. */
+MOE_API int moe_router_topk(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
+                    const float *b_router, int T, int d, int E, int k, float *route);
+
+/* moeUp: act[t·k + s] = clampedSwiglu(x[t]·glu[e] + glu.bias[e],
+ * x[t]·lin[e] + lin.bias[e]), e = route[t, s]. x [T, K] (f32, or f16 as an
+ * extension), act f32 [T·k, N]. The two biases are passed apart (the
+ * reference concatenates them per forward, ops/matmul.ts:240). */
+MOE_API int moe_up(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *route,
+           const moe_expert_weight *glu, const moe_expert_weight *lin, int T, int K, int N,
+           int E, int k, int bits, int group_size, float *act);
+
+/* moeDown: out[t] = residual[t] + Σ_s gate_s·(act[t·k + s]·w[e_s] + bias[e_s]).
+ * act f32 [T·k, K], residual f32 [T, N] or NULL, out f32 [T, N]. */
+MOE_API int moe_down(moe_ctx *ctx, const float *act, const float *route, const moe_expert_weight *down,
+             const float *residual, int T, int K, int N, int E, int k, int bits,
+             int group_size, float *out);
+
+/* The whole routed layer in one call: router+topk → dispatch → grouped
+ * gate/up+SwiGLU → grouped down → weighted combine + residual.
+ * x [T, d] f32/f16; router W f32 [d, E], b [E] or NULL; glu/lin K = d,
+ * N = I; down K = I, N = d; residual f32 [T, d] or NULL; route_out f32
+ * [T, 2k] or NULL; out f32 [T, d]. group_size_up divides d, group_size_down
+ * divides I (d and I themselves for one scale per output channel). */
+MOE_API int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
+              const float *b_router, const moe_expert_weight *glu, const moe_expert_weight *lin,
+              const moe_expert_weight *down, const float *residual, int T, int d, int I, int E,
+              int k, int bits, int group_size_up, int group_size_down, float *route_out,
+              float *out);
+
+/* Test and diagnostic hook: the dispatch permutation of a route, as the
+ * layer builds it. perm [T·k] (sorted position → assignment t·k + s, −1
+ * past the valid ones), offsets [E + 1]. No reference counterpart: the
+ * reference has no permutation (moeQuantW.ts:131-134); exposed so its
+ * bit-exactness can be checked. */
+MOE_API int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int k, int32_t *perm,
+                 int32_t *offsets);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RUNNTIME_MOE_H */

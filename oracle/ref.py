@@ -1,0 +1,149 @@
+"""numpy front end of the C oracle (moe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY — the checker for the HIP kernels; only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may use it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import build as _build
+
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+class _Opt:
+    """ndpointer that also accepts None (a NULL pointer)."""
+
+    def __init__(self, base):
+        self.base = base
+
+    def from_param(self, v):
+        if v is None:
+            return None
+        return self.base.from_param(v)
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_build.OUT):
+        _build.build()
+    L = ctypes.CDLL(_build.OUT)
+    I, I64, U32 = ctypes.c_int, ctypes.c_int64, ctypes.c_uint32
+    F = _Opt(_f32p)
+    sigs = {
+        "orc_lcg_f32": [_f32p, I64, U32],
+        "orc_pack_quantw_nk": [_i8p, I, I, I, _u32p],
+        "orc_pack_quantw_ekn": [_i8p, I, I, I, I, _u32p],
+        "orc_unpack_quantw": [_u32p, I, I, I, I, _i8p],
+        "orc_topk": [_f32p, I, I, I, _f32p],
+        "orc_router_logits": [_f32p, _f32p, F, I, I, I, _f32p],
+        "orc_moe_up_f64": [_f32p, _f32p, _u32p, _f32p, F, _u32p, _f32p, F, I, I, I, I, I, I, I,
+                           _f32p],
+        "orc_moe_down_f64": [_f32p, _f32p, _u32p, _f32p, F, F, I, I, I, I, I, I, I, _f32p],
+        "orc_moe_up_f32ref": [_f32p, _f32p, _u32p, _f32p, F, _u32p, _f32p, F, I, I, I, I, I, I,
+                              I, _f32p],
+        "orc_moe_down_f32ref": [_f32p, _f32p, _u32p, _f32p, F, F, I, I, I, I, I, I, I, _f32p],
+        "orc_dispatch": [_f32p, I, I, I, _i32p, _i32p, _i32p],
+        "orc_moe_layer_f64": [_f32p, _f32p, F, _u32p, _f32p, F, _u32p, _f32p, F, _u32p, _f32p, F,
+                              F, I, I, I, I, I, I, I, I, _f32p, _f32p, _f32p],
+    }
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = None
+    L.orc_swiglu_f64.argtypes = [ctypes.c_double, ctypes.c_double]
+    L.orc_swiglu_f64.restype = ctypes.c_double
+    _lib = L
+    return L
+
+
+def _f(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def lcg_f32(n, seed):
+    out = np.empty(n, np.float32)
+    lib().orc_lcg_f32(out, n, seed)
+    return out
+
+
+def pack_nk(ints_nk, k, n, bits):
+    words = np.zeros(k * n * bits // 32, np.uint32)
+    lib().orc_pack_quantw_nk(np.ascontiguousarray(ints_nk, np.int8), k, n, bits, words)
+    return words
+
+
+def pack_ekn(q, bits):
+    E, K, N = q.shape
+    words = np.zeros(E * K * N * bits // 32, np.uint32)
+    lib().orc_pack_quantw_ekn(np.ascontiguousarray(q, np.int8), E, K, N, bits, words)
+    return words
+
+
+def unpack(words, E, K, N, bits):
+    q = np.zeros((E, K, N), np.int8)
+    lib().orc_unpack_quantw(np.ascontiguousarray(words, np.uint32), E, K, N, bits, q)
+    return q
+
+
+def topk(logits, k):
+    T, E = logits.shape
+    route = np.zeros((T, 2 * k), np.float32)
+    lib().orc_topk(_f(logits), T, E, k, route)
+    return route
+
+
+def router_logits(x, w, b=None):
+    T, d = x.shape
+    E = w.shape[1]
+    out = np.zeros((T, E), np.float32)
+    lib().orc_router_logits(_f(x), _f(w), _f(b), T, d, E, out)
+    return out
+
+
+def swiglu(g, l):
+    return lib().orc_swiglu_f64(float(g), float(l))
+
+
+def moe_up(x, route, glu, lin, bits, g, E, f32ref=False):
+    """glu/lin: (words uint32, scales f32 [E·K/g, N], bias f32 [E, N] or None)."""
+    T, K = x.shape
+    k = route.shape[1] // 2
+    N = glu[1].shape[-1]
+    act = np.zeros((T * k, N), np.float32)
+    fn = lib().orc_moe_up_f32ref if f32ref else lib().orc_moe_up_f64
+    fn(_f(x), _f(route), np.ascontiguousarray(glu[0], np.uint32), _f(glu[1]), _f(glu[2]),
+       np.ascontiguousarray(lin[0], np.uint32), _f(lin[1]), _f(lin[2]), T, K, N, E, k, bits, g,
+       act)
+    return act
+
+
+def moe_down(act, route, down, residual, bits, g, E, f32ref=False):
+    rows, K = act.shape
+    k = route.shape[1] // 2
+    T = rows // k
+    N = down[1].shape[-1]
+    out = np.zeros((T, N), np.float32)
+    fn = lib().orc_moe_down_f32ref if f32ref else lib().orc_moe_down_f64
+    fn(_f(act), _f(route), np.ascontiguousarray(down[0], np.uint32), _f(down[1]), _f(down[2]),
+       _f(residual), T, K, N, E, k, bits, g, out)
+    return out
+
+
+def dispatch(route, E):
+    T = route.shape[0]
+    k = route.shape[1] // 2
+    perm = np.zeros(T * k, np.int32)
+    inv = np.zeros(T * k, np.int32)
+    offsets = np.zeros(E + 1, np.int32)
+    lib().orc_dispatch(_f(route), T, k, E, perm, inv, offsets)
+    return perm, inv, offsets

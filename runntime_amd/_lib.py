@@ -1,0 +1,91 @@
+"""Loads libmoe.so and declares its C ABI (include/runntime_moe.h) for ctypes.
+
+The library must have been built (``python -m runntime_amd.build``); there is
+no fallback: without it every op raises RunntimeError('NOT_INITIALIZED').
+"""
+import ctypes
+import os
+import threading
+
+from .errors import STATUS_CODES, RunntimeError
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmoe.so")
+
+MOE_F32 = 0
+MOE_F16 = 1
+
+# Every symbol include/runntime_moe.h declares.
+EXPORTED = (
+    "moe_version", "moe_last_error", "moe_ctx_create", "moe_ctx_set_stream",
+    "moe_ctx_reserve", "moe_ctx_destroy", "moe_sync", "moe_topk", "moe_router_topk",
+    "moe_up", "moe_down", "moe_layer", "moe_dispatch",
+)
+
+
+class ExpertWeightC(ctypes.Structure):
+    """moe_expert_weight: quantW words, f32 scales, f32 bias (or NULL)."""
+    _fields_ = [("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("bias", ctypes.c_void_p)]
+
+
+_lock = threading.Lock()
+_lib = None
+_ctxs = {}
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, with argument types declared."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RunntimeError(
+                "NOT_INITIALIZED",
+                f"{LIB_PATH} is not built; run `python -m runntime_amd.build`")
+        lib = ctypes.CDLL(LIB_PATH)
+        P, I, V = ctypes.c_void_p, ctypes.c_int, None
+        W = ctypes.POINTER(ExpertWeightC)
+        sigs = {
+            "moe_version": ([], I),
+            "moe_last_error": ([], ctypes.c_char_p),
+            "moe_ctx_create": ([I, P, ctypes.POINTER(P)], I),
+            "moe_ctx_set_stream": ([P, P], I),
+            "moe_ctx_reserve": ([P, I, I, I, I, I], I),
+            "moe_ctx_destroy": ([P], I),
+            "moe_sync": ([P], I),
+            "moe_topk": ([P, P, I, I, I, I, P], I),
+            "moe_router_topk": ([P, P, I, P, P, I, I, I, I, P], I),
+            "moe_up": ([P, P, I, P, W, W, I, I, I, I, I, I, I, P], I),
+            "moe_down": ([P, P, P, W, P, I, I, I, I, I, I, I, P], I),
+            "moe_layer": ([P, P, I, P, P, W, W, W, P, I, I, I, I, I, I, I, I, P, P], I),
+            "moe_dispatch": ([P, P, I, I, I, P, P], I),
+        }
+        for name, (args, res) in sigs.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    """Raises the RunntimeError a non-zero moe_status stands for."""
+    if rc == 0:
+        return
+    msg = load().moe_last_error().decode("utf-8", "replace")
+    raise RunntimeError(STATUS_CODES.get(rc, "EXECUTION_FAILED"), msg)
+
+
+def context(device: int, stream_handle: int) -> int:
+    """The library context of `device`, switched to enqueue on `stream_handle`
+    (a hipStream_t as an int, 0 for the context's own stream)."""
+    lib = load()
+    with _lock:
+        ctx = _ctxs.get(device)
+        if ctx is None:
+            out = ctypes.c_void_p()
+            check(lib.moe_ctx_create(device, None, ctypes.byref(out)))
+            ctx = out.value
+            _ctxs[device] = ctx
+    check(lib.moe_ctx_set_stream(ctx, stream_handle or None))
+    return ctx

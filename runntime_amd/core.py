@@ -1,0 +1,266 @@
+"""The MoE ops of `runntime/core`, on MI355X.
+
+Same names, argument meaning and error messages as the reference's
+graph ops (packages/runntime/src/core/graph/ops/):
+  topk(x, k)                                  reduce.ts:93-100
+  moeUp(x, route, glu, lin, {bits, groupSize})  matmul.ts:220-244
+  moeDown(act, route, out, residual, opts)    matmul.ts:246-272
+plus the fused layer (EagerMoeMlp's quantized branch, zoo/privacy-filter/
+moeMlp.ts:82-121) and the router+topk fusion.
+
+The reference builds lazy nodes and runs them later; here each op enqueues
+its HIP kernels at once on torch's current stream and returns the output
+tensor (the graph/executor layer is the caller's). Tensors are torch
+tensors on a ROCm device; quantW weights are `QuantW` values.
+
+Generalisation: the reference compiles in k = 4 experts per token. Here k
+is 1..16; `topk` takes it, moeUp/moeDown read it from the route's
+[T, 2k] shape. At k = 4 everything reduces to the reference's behaviour.
+"""
+import ctypes
+import json
+
+import torch
+
+from . import _lib
+from .errors import RunntimeError
+from .quantw import QuantExpertWeight, QuantW
+
+MAX_K = 16
+
+
+def _dims(t):
+    return list(t.dims) if isinstance(t, QuantW) else list(t.shape)
+
+
+def _dtype_name(t) -> str:
+    if isinstance(t, QuantW):
+        return "quantW"
+    return {torch.float32: "f32", torch.float16: "f16", torch.int32: "i32"}.get(t.dtype, str(t.dtype))
+
+
+def _want2d(name, x, allow):
+    """wantND(name, x, 2, allow) (src/core/graph/ops/shared.ts:46-70)."""
+    dims = _dims(x)
+    dt = _dtype_name(x)
+    if len(dims) != 2 or dt not in allow:
+        raise ValueError(
+            f"{name}: expected a 2D {' or '.join(allow)} tensor, got "
+            f"dims={json.dumps(dims, separators=(',', ':'))} dtype={dt}")
+    return dims[0], dims[1], dt
+
+
+def _route_k(route) -> int:
+    """k of a [T, 2k] route, or the reference's 4 when the shape is not one."""
+    dims = _dims(route)
+    if len(dims) == 2 and dims[1] % 2 == 0 and 1 <= dims[1] // 2 <= MAX_K:
+        return dims[1] // 2
+    return 4
+
+
+def _check_expert_weight(op, wt: QuantExpertWeight, k_in: int, route, t: int, k: int, opts):
+    """checkExpertWeight (src/core/graph/ops/matmul.ts:274-315). Returns
+    (N, experts)."""
+    bits, group_size = opts["bits"], opts["groupSize"]
+    if bits not in (8, 4):
+        raise ValueError(f"{op}: bits must be 8 or 4, got {bits}")
+    w = wt.w
+    wd = w.dims if isinstance(w, QuantW) else None
+    if not isinstance(w, QuantW) or len(wd) != 2 or wd[0] % k_in != 0:
+        raise ValueError(f"{op}: w must be a quantW [E·{k_in}, N] weight")
+    r, n = wd
+    experts = r // k_in
+    if w.elems != (r * n * bits) // 32:
+        raise ValueError(f"{op}: quantW weight elems {w.elems} != rows·cols·{bits}/32")
+    if k_in % 4 != 0 or n % 4 != 0:
+        raise ValueError(f"{op}: K {k_in} and N {n} must be multiples of 4")
+    if group_size <= 0 or group_size % 4 != 0 or k_in % group_size != 0:
+        raise ValueError(
+            f"{op}: groupSize {group_size} must be a multiple of 4 that divides K {k_in}")
+    sc = wt.scales
+    if _dtype_name(sc) != "f32" or sc.numel() != (experts * k_in * n) // group_size:
+        raise ValueError(f"{op}: scales must be f32 [{(experts * k_in) // group_size}, {n}]")
+    b = wt.bias
+    if b is not None and (_dtype_name(b) != "f32" or b.numel() != experts * n):
+        raise ValueError(f"{op}: bias must be f32 [{experts}, {n}]")
+    rd = _dims(route)
+    if _dtype_name(route) != "f32" or len(rd) != 2 or rd[0] != t or rd[1] != 2 * k:
+        raise ValueError(f"{op}: route must be topk's f32 [{t}, {2 * k}] output")
+    return n, experts
+
+
+def _device_of(*tensors) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        tt = t.words if isinstance(t, QuantW) else t
+        if tt.device.type != "cuda":
+            raise RunntimeError("INVALID_ARGUMENT",
+                                f"tensors must be on a ROCm device, got {tt.device}")
+        if dev is None:
+            dev = tt.device
+        elif tt.device != dev:
+            raise RunntimeError("INVALID_ARGUMENT", "tensors are on different devices")
+        if tt.numel() == 0:
+            raise RunntimeError("INVALID_ARGUMENT", "tensor: the shape has no elements")
+        if not tt.is_contiguous():
+            raise RunntimeError("INVALID_ARGUMENT", "tensors must be contiguous")
+    return dev
+
+
+def _ctx(dev: torch.device) -> int:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(idx).cuda_stream
+    return _lib.context(idx, stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return (t.words if isinstance(t, QuantW) else t).data_ptr()
+
+
+def _weight_c(wt: QuantExpertWeight) -> _lib.ExpertWeightC:
+    return _lib.ExpertWeightC(_ptr(wt.w), _ptr(wt.scales), _ptr(wt.bias))
+
+
+def _xdtype(t) -> int:
+    return _lib.MOE_F16 if t.dtype == torch.float16 else _lib.MOE_F32
+
+
+# ----------------------------------------------------------------- the ops
+
+
+def topk(x: torch.Tensor, k: int) -> torch.Tensor:
+    """Router top-k plus softmax over the selected logits, lowest index on
+    ties. Returns f32 [M, 2k]: ids first, then weights, descending by logit
+    (reduce.ts:93-100; kernel topkSelect.ts:21-92)."""
+    m, n, _ = _want2d("topk", x, ("f32", "f16"))
+    if not (1 <= k <= MAX_K):
+        raise ValueError(f"topk: k must be in 1..{MAX_K}, got {k}")
+    if n < k:
+        raise ValueError(f"topk: need at least {k} columns, got {n}")
+    dev = _device_of(x)
+    route = torch.empty((m, 2 * k), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_topk(_ctx(dev), x.data_ptr(), _xdtype(x), m, n, k, route.data_ptr()))
+    return route
+
+
+def router_topk(x: torch.Tensor, w: torch.Tensor, b, k: int) -> torch.Tensor:
+    """topk(linear(x, w, b), k) fused: x [T, d] f32/f16, w f32 [d, E] (the
+    router Linear's weight after the load-time transpose,
+    src/core/nn/layers.ts:176-217), b f32 [E] or None. Logits use this
+    library's canonical f32 summation order."""
+    t, d, _ = _want2d("router", x, ("f32", "f16"))
+    wd = _dims(w)
+    if _dtype_name(w) != "f32" or len(wd) != 2 or wd[0] != d:
+        raise ValueError(f"router: weight must be f32 [{d}, E]")
+    e = wd[1]
+    if b is not None and (_dtype_name(b) != "f32" or b.numel() != e):
+        raise ValueError(f"router: bias must be f32 [{e}]")
+    if not (1 <= k <= MAX_K):
+        raise ValueError(f"topk: k must be in 1..{MAX_K}, got {k}")
+    if e < k:
+        raise ValueError(f"topk: need at least {k} columns, got {e}")
+    dev = _device_of(x, w, b)
+    route = torch.empty((t, 2 * k), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_router_topk(_ctx(dev), x.data_ptr(), _xdtype(x), w.data_ptr(), _ptr(b), t,
+                                   d, e, k, route.data_ptr()))
+    return route
+
+
+def moeUp(x, route, glu: QuantExpertWeight, lin: QuantExpertWeight, opts) -> torch.Tensor:
+    """MoE input projections and clamped SwiGLU. route is topk's [T, 2k]. For
+    token t and slot s with expert e, row t·k + s of the [T·k, N] result is
+    swiglu(x[t]·glu.w[e] + glu.bias[e], x[t]·lin.w[e] + lin.bias[e])
+    (src/core/graph/ops/matmul.ts:220-244). x is f32 as in the reference;
+    f16 is accepted too."""
+    t, kin, _ = _want2d("moeUp", x, ("f32", "f16"))
+    k = _route_k(route)
+    n, experts = _check_expert_weight("moeUp", glu, kin, route, t, k, opts)
+    _check_expert_weight("moeUp", lin, kin, route, t, k, opts)
+    if lin.w.dims[0] != glu.w.dims[0] or lin.w.dims[1] != n:
+        raise ValueError("moeUp: glu and lin weights must have the same shape")
+    dev = _device_of(x, route, glu.w, glu.scales, glu.bias, lin.w, lin.scales, lin.bias)
+    act = torch.empty((t * k, n), dtype=torch.float32, device=dev)
+    g, l_ = _weight_c(glu), _weight_c(lin)
+    lib = _lib.load()
+    _lib.check(lib.moe_up(_ctx(dev), x.data_ptr(), _xdtype(x), route.data_ptr(), ctypes.byref(g),
+                          ctypes.byref(l_), t, kin, n, experts, k, opts["bits"],
+                          opts["groupSize"], act.data_ptr()))
+    return act
+
+
+def moeDown(act, route, out: QuantExpertWeight, residual, opts) -> torch.Tensor:
+    """MoE output projection. Mixes the k slots by gate weight and adds the
+    residual: out[t] = residual[t] + Σ_s gate_s·(act[t·k + s]·w[e_s] + bias[e_s])
+    (src/core/graph/ops/matmul.ts:246-272). act is moeUp's [T·k, K]; out is
+    [T, N]."""
+    rows, kin, _ = _want2d("moeDown", act, ("f32",))
+    k = _route_k(route)
+    if rows % k != 0:
+        raise ValueError(f"moeDown: act rows {rows} must be a multiple of {k}")
+    t = rows // k
+    n, experts = _check_expert_weight("moeDown", out, kin, route, t, k, opts)
+    if residual is not None and (_dtype_name(residual) != "f32" or residual.numel() != t * n):
+        raise ValueError(f"moeDown: residual must be f32 [{t}, {n}]")
+    dev = _device_of(act, route, out.w, out.scales, out.bias, residual)
+    y = torch.empty((t, n), dtype=torch.float32, device=dev)
+    w = _weight_c(out)
+    lib = _lib.load()
+    _lib.check(lib.moe_down(_ctx(dev), act.data_ptr(), route.data_ptr(), ctypes.byref(w),
+                            _ptr(residual), t, kin, n, experts, k, opts["bits"],
+                            opts["groupSize"], y.data_ptr()))
+    return y
+
+
+def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWeight,
+              down: QuantExpertWeight, residual, k: int, bits: int = 8,
+              group_size_up=None, group_size_down=None, return_route: bool = False):
+    """The routed layer in one call (EagerMoeMlp.forward's quantized branch
+    after the norm, zoo/privacy-filter/moeMlp.ts:82-121):
+    route = topk(x·Wr + br, k); act = moeUp(x, route, glu, lin);
+    out = moeDown(act, route, down, residual). Group sizes default to one
+    scale per output channel (K of each projection)."""
+    t, d, _ = _want2d("moe_layer", x, ("f32", "f16"))
+    rw = _dims(router_w)
+    if _dtype_name(router_w) != "f32" or len(rw) != 2 or rw[0] != d:
+        raise ValueError(f"moe_layer: router weight must be f32 [{d}, E]")
+    e = rw[1]
+    if not isinstance(glu.w, QuantW) or glu.w.dims[0] != e * d:
+        raise ValueError(f"moe_layer: glu.w must be a quantW [E·{d}, I] weight")
+    i = glu.w.dims[1]
+    gu = group_size_up or d
+    gd = group_size_down or i
+    route = torch.empty((t, 2 * k), dtype=torch.float32, device=x.device)
+    _check_expert_weight("moe_layer", glu, d, route, t, k, {"bits": bits, "groupSize": gu})
+    _check_expert_weight("moe_layer", lin, d, route, t, k, {"bits": bits, "groupSize": gu})
+    _check_expert_weight("moe_layer", down, i, route, t, k, {"bits": bits, "groupSize": gd})
+    if residual is not None and (_dtype_name(residual) != "f32" or residual.numel() != t * d):
+        raise ValueError(f"moe_layer: residual must be f32 [{t}, {d}]")
+    dev = _device_of(x, router_w, router_b, glu.w, lin.w, down.w, residual)
+    out = torch.empty((t, d), dtype=torch.float32, device=dev)
+    g, l_, dn = _weight_c(glu), _weight_c(lin), _weight_c(down)
+    lib = _lib.load()
+    _lib.check(lib.moe_layer(_ctx(dev), x.data_ptr(), _xdtype(x), router_w.data_ptr(),
+                             _ptr(router_b), ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn),
+                             _ptr(residual), t, d, i, e, k, bits, gu, gd, route.data_ptr(),
+                             out.data_ptr()))
+    return (out, route) if return_route else out
+
+
+def dispatch(route, num_experts: int):
+    """The dispatch permutation the layer builds for `route` (diagnostic):
+    (perm int32 [T·k], offsets int32 [E + 1])."""
+    t, c = _dims(route)
+    k = c // 2
+    dev = _device_of(route)
+    perm = torch.empty(t * k, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_dispatch(_ctx(dev), route.data_ptr(), t, num_experts, k, perm.data_ptr(),
+                                offsets.data_ptr()))
+    return perm, offsets

@@ -1,0 +1,321 @@
+// C ABI of libmoe.so: argument checks, the context and its workspace, and the
+// order of kernel launches for each op. Declarations and the reference
+// interface each entry replaces are in include/runntime_moe.h.
+#include <stdio.h>
+
+#include <string>
+
+#include "moe_internal.h"
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_last_error;
+
+void moe_set_error(const std::string &msg) { g_last_error = msg; }
+
+int moe_fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+extern "C" const char *moe_last_error(void) { return g_last_error.c_str(); }
+extern "C" int moe_version(void) { return MOE_VERSION; }
+
+// ------------------------------------------------------------------ context
+
+extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
+  if (!out) return moe_fail(MOE_INVALID_ARGUMENT, "moe_ctx_create: out is NULL");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+    return moe_fail(MOE_NOT_INITIALIZED, "moe_ctx_create: no HIP device is visible");
+  if (device < 0 || device >= n)
+    return moe_fail(MOE_INVALID_ARGUMENT, "moe_ctx_create: device " + std::to_string(device) +
+                                              " out of range (" + std::to_string(n) + " visible)");
+  MOE_HIP_CHECK(hipSetDevice(device));
+  moe_ctx *c = new moe_ctx();
+  c->device = device;
+  if (stream) {
+    c->stream = (hipStream_t)stream;
+  } else {
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete c;
+      return moe_fail(MOE_EXECUTION_FAILED,
+                      std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    c->stream = c->own_stream;
+  }
+  *out = c;
+  return MOE_OK;
+}
+
+static int check_ctx(moe_ctx *ctx, const char *op) {
+  if (!ctx) return moe_fail(MOE_NOT_INITIALIZED, std::string(op) + ": context is NULL");
+  if (ctx->disposed) return moe_fail(MOE_RESOURCE_DISPOSED, std::string(op) + ": context disposed");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess)
+    return moe_fail(MOE_EXECUTION_FAILED, std::string("hipSetDevice: ") + hipGetErrorString(e));
+  return MOE_OK;
+}
+
+extern "C" int moe_ctx_set_stream(moe_ctx *ctx, void *stream) {
+  int rc = check_ctx(ctx, "moe_ctx_set_stream");
+  if (rc) return rc;
+  ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
+  if (!ctx->stream) {
+    MOE_HIP_CHECK(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking));
+    ctx->stream = ctx->own_stream;
+  }
+  return MOE_OK;
+}
+
+int moe_ws_ensure(moe_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->ws_size) return MOE_OK;
+  // Work already queued may still read the old workspace.
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  if (ctx->ws) MOE_HIP_CHECK(hipFree(ctx->ws));
+  ctx->ws = nullptr;
+  ctx->ws_size = 0;
+  size_t want = bytes + bytes / 4;
+  MOE_HIP_CHECK(hipMalloc((void **)&ctx->ws, want));
+  ctx->ws_size = want;
+  return MOE_OK;
+}
+
+extern "C" int moe_ctx_destroy(moe_ctx *ctx) {
+  if (!ctx) return MOE_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  ctx->disposed = true;
+  delete ctx;
+  return MOE_OK;
+}
+
+extern "C" int moe_sync(moe_ctx *ctx) {
+  int rc = check_ctx(ctx, "moe_sync");
+  if (rc) return rc;
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  MOE_HIP_CHECK(hipGetLastError());
+  return MOE_OK;
+}
+
+// ---------------------------------------------------------------- checks
+
+#define REQUIRE(cond, msg)                                   \
+  do {                                                       \
+    if (!(cond)) return moe_fail(MOE_INVALID_ARGUMENT, msg); \
+  } while (0)
+
+static std::string S(long v) { return std::to_string(v); }
+
+static int check_k(const char *op, int k, int E) {
+  REQUIRE(k >= 1 && k <= MAX_K, std::string(op) + ": k must be in 1.." + S(MAX_K) + ", got " + S(k));
+  REQUIRE(E >= k, std::string(op) + ": need at least " + S(k) + " columns, got " + S(E));
+  return MOE_OK;
+}
+
+// checkExpertWeight (src/core/graph/ops/matmul.ts:274-315).
+static int check_weight(const char *op, const moe_expert_weight *w, int K, int N, int E, int bits,
+                        int g) {
+  std::string o(op);
+  REQUIRE(bits == 8 || bits == 4, o + ": bits must be 8 or 4, got " + S(bits));
+  REQUIRE(w && w->w, o + ": w must be a quantW [E·" + S(K) + ", N] weight");
+  REQUIRE(K % 4 == 0 && N % 4 == 0,
+          o + ": K " + S(K) + " and N " + S(N) + " must be multiples of 4");
+  REQUIRE(g > 0 && g % 4 == 0 && K % g == 0,
+          o + ": groupSize " + S(g) + " must be a multiple of 4 that divides K " + S(K));
+  REQUIRE(w->scales, o + ": scales must be f32 [" + S((long)E * K / g) + ", " + S(N) + "]");
+  REQUIRE(E >= 1 && E <= 1024, o + ": expert count must be in 1..1024, got " + S(E));
+  return MOE_OK;
+}
+
+// ------------------------------------------------------------- dispatch ws
+
+struct LayerWs {
+  DispatchBufs db;
+  float *route = nullptr;
+  float *partial = nullptr;
+  float *act = nullptr;
+  float *y = nullptr;
+};
+
+// Workspace for a call over T tokens (A = T·k assignments). Sections that a
+// call does not need have size 0.
+static int plan_ws(moe_ctx *ctx, int T, int k, int E, size_t route_floats, size_t partial_floats,
+                   size_t act_floats, size_t y_floats, LayerWs &L) {
+  int A = T * k;
+  int nblk = (A + DISPATCH_TILE - 1) / DISPATCH_TILE;
+  WsPlan p;
+  size_t o_cnt = p.take(sizeof(int32_t) * (size_t)nblk * E);
+  size_t o_base = p.take(sizeof(int32_t) * (size_t)nblk * E);
+  size_t o_off = p.take(sizeof(int32_t) * (E + 1));
+  size_t o_toff = p.take(sizeof(int32_t) * (E + 1));
+  size_t o_act_list = p.take(sizeof(int32_t) * E);
+  size_t o_meta = p.take(sizeof(int32_t) * META_N);
+  size_t o_perm = p.take(sizeof(int32_t) * (size_t)A);
+  size_t o_route = p.take(sizeof(float) * route_floats);
+  size_t o_part = p.take(sizeof(float) * partial_floats);
+  size_t o_actv = p.take(sizeof(float) * act_floats);
+  size_t o_y = p.take(sizeof(float) * y_floats);
+  int rc = moe_ws_ensure(ctx, p.off);
+  if (rc) return rc;
+  char *b = ctx->ws;
+  L.db.blk_counts = (int32_t *)(b + o_cnt);
+  L.db.blk_base = (int32_t *)(b + o_base);
+  L.db.offsets = (int32_t *)(b + o_off);
+  L.db.tile_off = (int32_t *)(b + o_toff);
+  L.db.active = (int32_t *)(b + o_act_list);
+  L.db.meta = (int32_t *)(b + o_meta);
+  L.db.perm = (int32_t *)(b + o_perm);
+  L.route = route_floats ? (float *)(b + o_route) : nullptr;
+  L.partial = partial_floats ? (float *)(b + o_part) : nullptr;
+  L.act = act_floats ? (float *)(b + o_actv) : nullptr;
+  L.y = y_floats ? (float *)(b + o_y) : nullptr;
+  return MOE_OK;
+}
+
+static constexpr int TILE_M = 128;
+
+static int after_launch(const char *op) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return moe_fail(MOE_EXECUTION_FAILED, std::string(op) + ": launch failed: " + hipGetErrorString(e));
+  return MOE_OK;
+}
+
+// ------------------------------------------------------------------- ops
+
+extern "C" int moe_topk(moe_ctx *ctx, const void *logits, moe_dtype dtype, int T, int E, int k,
+                        float *route) {
+  int rc = check_ctx(ctx, "topk");
+  if (rc) return rc;
+  if ((rc = check_k("topk", k, E))) return rc;
+  REQUIRE(T >= 1, "topk: T must be at least 1, got " + S(T));
+  REQUIRE(E <= TOPK_MAX_E, "topk: more than " + S(TOPK_MAX_E) + " columns");
+  REQUIRE(logits && route, "topk: NULL tensor");
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "topk: dtype must be f32 or f16");
+  if ((rc = launch_topk(logits, dtype, T, E, k, route, ctx->stream))) return rc;
+  return after_launch("topk");
+}
+
+extern "C" int moe_router_topk(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
+                               const float *w_router, const float *b_router, int T, int d, int E,
+                               int k, float *route) {
+  int rc = check_ctx(ctx, "router_topk");
+  if (rc) return rc;
+  if ((rc = check_k("router_topk", k, E))) return rc;
+  REQUIRE(T >= 1 && d >= 1, "router_topk: T and d must be positive");
+  REQUIRE(E <= ROUTER_MAX_E, "router_topk: more than " + S(ROUTER_MAX_E) + " experts");
+  REQUIRE(x && w_router && route, "router_topk: NULL tensor");
+  int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  WsPlan p;
+  p.take(sizeof(float) * (size_t)T * J * E);
+  if ((rc = moe_ws_ensure(ctx, p.off))) return rc;
+  if ((rc = launch_router_topk(x, x_dtype, w_router, b_router, T, d, E, k, (float *)ctx->ws, route,
+                               ctx->stream)))
+    return rc;
+  return after_launch("router_topk");
+}
+
+extern "C" int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int k, int32_t *perm,
+                            int32_t *offsets) {
+  int rc = check_ctx(ctx, "dispatch");
+  if (rc) return rc;
+  if ((rc = check_k("dispatch", k, E))) return rc;
+  REQUIRE(T >= 1 && E <= 1024, "dispatch: T ≥ 1 and E ≤ 1024 required");
+  LayerWs L;
+  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, 0, L))) return rc;
+  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
+  if (perm)
+    MOE_HIP_CHECK(hipMemcpyAsync(perm, L.db.perm, sizeof(int32_t) * (size_t)T * k,
+                                 hipMemcpyDeviceToDevice, ctx->stream));
+  if (offsets)
+    MOE_HIP_CHECK(hipMemcpyAsync(offsets, L.db.offsets, sizeof(int32_t) * (E + 1),
+                                 hipMemcpyDeviceToDevice, ctx->stream));
+  return after_launch("dispatch");
+}
+
+extern "C" int moe_up(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *route,
+                      const moe_expert_weight *glu, const moe_expert_weight *lin, int T, int K,
+                      int N, int E, int k, int bits, int group_size, float *act) {
+  int rc = check_ctx(ctx, "moeUp");
+  if (rc) return rc;
+  if ((rc = check_k("moeUp", k, E))) return rc;
+  if ((rc = check_weight("moeUp", glu, K, N, E, bits, group_size))) return rc;
+  if ((rc = check_weight("moeUp", lin, K, N, E, bits, group_size))) return rc;
+  REQUIRE(T >= 1, "moeUp: T must be at least 1");
+  REQUIRE(x && route && act, "moeUp: NULL tensor");
+  LayerWs L;
+  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, 0, L))) return rc;
+  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
+  // Rows of ids that are not experts stay zero (the reference leaves them
+  // undefined).
+  if ((rc = launch_zero(act, (size_t)T * k * N, ctx->stream))) return rc;
+  ExpertArgs ea{MODE_UP, x, x_dtype, k, route, k, glu, lin, K, N, E, bits, group_size, act, T * k};
+  if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
+  return after_launch("moeUp");
+}
+
+extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
+                        const moe_expert_weight *down, const float *residual, int T, int K, int N,
+                        int E, int k, int bits, int group_size, float *out) {
+  int rc = check_ctx(ctx, "moeDown");
+  if (rc) return rc;
+  if ((rc = check_k("moeDown", k, E))) return rc;
+  if ((rc = check_weight("moeDown", down, K, N, E, bits, group_size))) return rc;
+  REQUIRE(T >= 1, "moeDown: T must be at least 1");
+  REQUIRE(act && route && out, "moeDown: NULL tensor");
+  LayerWs L;
+  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, (size_t)T * k * N, L))) return rc;
+  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
+  ExpertArgs ea{MODE_DOWN, act, MOE_F32, 1, route, k, down, nullptr, K, N, E, bits, group_size,
+                L.y, T * k};
+  if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
+  if ((rc = launch_combine(L.y, route, residual, T, N, E, k, out, ctx->stream))) return rc;
+  return after_launch("moeDown");
+}
+
+extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
+                         const float *b_router, const moe_expert_weight *glu,
+                         const moe_expert_weight *lin, const moe_expert_weight *down,
+                         const float *residual, int T, int d, int I, int E, int k, int bits,
+                         int group_size_up, int group_size_down, float *route_out, float *out) {
+  int rc = check_ctx(ctx, "moe_layer");
+  if (rc) return rc;
+  if ((rc = check_k("moe_layer", k, E))) return rc;
+  if ((rc = check_weight("moe_layer", glu, d, I, E, bits, group_size_up))) return rc;
+  if ((rc = check_weight("moe_layer", lin, d, I, E, bits, group_size_up))) return rc;
+  if ((rc = check_weight("moe_layer", down, I, d, E, bits, group_size_down))) return rc;
+  REQUIRE(T >= 1, "moe_layer: T must be at least 1");
+  REQUIRE(E <= ROUTER_MAX_E, "moe_layer: more than " + S(ROUTER_MAX_E) + " experts");
+  REQUIRE(x && w_router && out, "moe_layer: NULL tensor");
+  const int A = T * k;
+  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  LayerWs L;
+  if ((rc = plan_ws(ctx, T, k, E, route_out ? 0 : (size_t)T * 2 * k, (size_t)T * J * E,
+                    (size_t)A * I, (size_t)A * d, L)))
+    return rc;
+  float *route = route_out ? route_out : L.route;
+  hipStream_t s = ctx->stream;
+  if ((rc = launch_router_topk(x, x_dtype, w_router, b_router, T, d, E, k, L.partial, route, s)))
+    return rc;
+  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, s))) return rc;
+  ExpertArgs up{MODE_UP, x, x_dtype, k, route, k, glu, lin, d, I, E, bits, group_size_up, L.act, A};
+  if ((rc = launch_expert(up, L.db, s))) return rc;
+  ExpertArgs dn{MODE_DOWN, L.act, MOE_F32, 1, route, k, down, nullptr, I, d, E, bits,
+                group_size_down, L.y, A};
+  if ((rc = launch_expert(dn, L.db, s))) return rc;
+  if ((rc = launch_combine(L.y, route, residual, T, d, E, k, out, s))) return rc;
+  return after_launch("moe_layer");
+}
+
+extern "C" int moe_ctx_reserve(moe_ctx *ctx, int T, int d, int I, int E, int k) {
+  int rc = check_ctx(ctx, "moe_ctx_reserve");
+  if (rc) return rc;
+  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  LayerWs L;
+  return plan_ws(ctx, T, k, E, (size_t)T * 2 * k, (size_t)T * J * E, (size_t)T * k * I,
+                 (size_t)T * k * (d > I ? d : I), L);
+}

@@ -1,0 +1,162 @@
+"""The C-ABI library and the host-side op checks, without a GPU.
+
+The library must load and export every entry point include/runntime_moe.h
+declares. The ops' argument checks mirror the reference's graph-op tests
+(test/core/graph/ops/matmul.test.ts:276-409, topkSelect.gpu.test.ts:92-98):
+they run before any device work, so CPU tensors exercise them."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import runntime_amd as rt
+from runntime_amd import _lib
+from runntime_amd.quantw import QuantExpertWeight, QuantW
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    with open(os.path.join(ROOT, "include", "runntime_moe.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"MOE_API\s+[\w\s\*]*?\b(moe_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_symbols()
+    assert set(names) == set(_lib.EXPORTED), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.moe_version() == 1
+
+
+def test_nm_dynamic_exports():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (moe_\w+)", out))
+    assert set(declared_symbols()) <= exported
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
+def test_ctx_without_device_is_not_initialized():
+    lib = _lib.load()
+    out = ctypes.c_void_p()
+    rc = lib.moe_ctx_create(0, None, ctypes.byref(out))
+    assert rc == 3  # MOE_NOT_INITIALIZED
+    assert b"no HIP device" in lib.moe_last_error()
+    with pytest.raises(rt.RunntimeError) as ei:
+        _lib.check(rc)
+    assert ei.value.code == "NOT_INITIALIZED"
+
+
+def test_null_context_is_rejected():
+    lib = _lib.load()
+    rc = lib.moe_sync(None)
+    assert rc == 3
+    rc = lib.moe_topk(None, None, 0, 1, 4, 4, None)
+    assert rc == 3
+
+
+# ------------------------------------------------- op checks (graph-build)
+
+
+def _input(dims, dtype=torch.float32):
+    return torch.zeros(dims, dtype=dtype)
+
+
+def _quant(rows, cols, bits=8):
+    return QuantW(torch.zeros(rows * cols * bits // 32, dtype=torch.int32), (rows, cols))
+
+
+MOE = {"bits": 8, "groupSize": 4}
+
+
+def _experts(k, n, bits=8):
+    # One routed layer for 2 experts of [K, N] (matmul.test.ts:283-287).
+    return QuantExpertWeight(_quant(2 * k, n, bits), _input([2 * k // 4, n]), _input([2, n]))
+
+
+ROUTE = _input([3, 8])
+X = _input([3, 8])
+GLU = _experts(8, 16)
+LIN = _experts(8, 16)
+
+
+@pytest.mark.parametrize("case", [
+    dict(x=_input([3, 8], torch.float64), error=r"expected a 2D f32 or f16 tensor"),
+    dict(glu=QuantExpertWeight(_input([16, 16]), GLU.scales, GLU.bias),
+         error=r"w must be a quantW \[E·8, N\] weight"),
+    dict(glu=QuantExpertWeight(_quant(12, 16), GLU.scales, GLU.bias),
+         error=r"w must be a quantW \[E·8, N\] weight"),
+    dict(glu=QuantExpertWeight(_quant(16, 16, 4), GLU.scales, GLU.bias),
+         error=r"elems 32 != rows·cols·8/32"),
+    dict(glu=_experts(8, 6), lin=_experts(8, 6), error=r"K 8 and N 6 must be multiples of 4"),
+    dict(opts={"groupSize": 3}, error=r"groupSize 3 must be a multiple of 4 that divides K 8"),
+    dict(glu=QuantExpertWeight(GLU.w, _input([2, 16]), GLU.bias), error=r"scales must be f32 \[4, 16\]"),
+    dict(glu=QuantExpertWeight(GLU.w, GLU.scales, _input([16])), error=r"bias must be f32 \[2, 16\]"),
+    dict(route=_input([3, 3]), error=r"route must be topk's f32 \[3, 8\] output"),
+    dict(lin=_experts(8, 8), error=r"glu and lin weights must have the same shape"),
+])
+def test_moe_up_rejects(case):
+    # matmul.test.ts:311-371 (f16 activations are accepted here: an extension)
+    x = case.get("x", X)
+    route = case.get("route", ROUTE)
+    glu = case.get("glu", GLU)
+    lin = case.get("lin", LIN)
+    opts = {**MOE, **case.get("opts", {})}
+    with pytest.raises(ValueError, match=case["error"]):
+        rt.moeUp(x, route, glu, lin, opts)
+
+
+ACT = _input([12, 16])
+OUT = _experts(16, 8)
+RES = _input([3, 8])
+
+
+@pytest.mark.parametrize("case", [
+    dict(act=_input([10, 16]), error=r"act rows 10 must be a multiple of 4"),
+    dict(residual=_input([3, 4]), error=r"residual must be f32 \[3, 8\]"),
+    dict(route=_input([2, 8]), error=r"route must be topk's f32 \[3, 8\] output"),
+    dict(out=QuantExpertWeight(OUT.w, OUT.scales, _input([3, 8])), error=r"bias must be f32 \[2, 8\]"),
+])
+def test_moe_down_rejects(case):
+    # matmul.test.ts:384-409
+    with pytest.raises(ValueError, match=case["error"]):
+        rt.moeDown(case.get("act", ACT), case.get("route", ROUTE), case.get("out", OUT),
+                   case.get("residual", RES), MOE)
+
+
+@pytest.mark.parametrize("k,cols,error", [
+    (0, 8, r"k must be in 1..16, got 0"),
+    (17, 32, r"k must be in 1..16, got 17"),
+    (4, 3, r"need at least 4 columns, got 3"),
+])
+def test_topk_rejects(k, cols, error):
+    # topkSelect.gpu.test.ts:92-98 (k = 2 is accepted here: the reference
+    # compiles in k = 4, this build takes k in 1..16)
+    with pytest.raises(ValueError, match=error):
+        rt.topk(_input([2, cols]), k)
+
+
+def test_cpu_tensors_are_rejected_after_checks():
+    x = _input([2, 8])
+    with pytest.raises(rt.RunntimeError) as ei:
+        rt.topk(x, 4)
+    assert ei.value.code == "INVALID_ARGUMENT"
+
+
+def test_runntime_error_codes():
+    e = rt.RunntimeError("EXECUTION_FAILED", "boom")
+    assert rt.is_runntime_error(e) and rt.is_runntime_error(e, "EXECUTION_FAILED")
+    assert not rt.is_runntime_error(e, "INVALID_ARGUMENT")
+    assert not rt.is_runntime_error(ValueError("x"))
+    with pytest.raises(ValueError):
+        rt.RunntimeError("NOPE", "x")

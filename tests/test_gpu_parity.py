@@ -1,0 +1,298 @@
+"""Parity of the HIP path (libmoe.so through the C ABI) with the CPU oracle.
+
+Bars: expert ids and the dispatch permutation bit-exact; route weights and
+outputs within |got − want| ≤ 2e-3 + 1e-2·|want| of the oracle's f64 result
+(the layer bar), and, where the reference's own kernel tests apply, within
+their tighter atol 1e-5·K, rtol 1e-4 (moeQuantW.gpu.test.ts:100,127)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import runntime_amd as rt
+from oracle import ref
+from runntime_amd.quantw import QuantExpertWeight, QuantW
+from runntime_amd.synth import CONFIGS, make_inputs
+from tests.helpers import assert_close, random_quant_weight, route_for
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def gpu(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy() if t.dtype != torch.int32 else t.cpu().numpy()
+
+
+def weight_pair(E, K, N, bits, g, seed, with_bias=True):
+    q, sc = random_quant_weight(E, K, N, bits, g, seed)
+    bias = ref.lcg_f32(E * N, seed + 2).reshape(E, N) if with_bias else None
+    words = ref.pack_ekn(q, bits)
+    dev = QuantExpertWeight(QuantW(gpu(words.view(np.int32)), (E * K, N)), gpu(sc),
+                            gpu(bias) if with_bias else None)
+    return dev, (words, sc, bias)
+
+
+# -------------------------------------------------------------------- topk
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("shape", [(3, 4), (7, 9), (65, 32), (5, 1000)])
+@pytest.mark.parametrize("k", [4, 1, 2, 8])
+def test_topk_shapes(dtype, shape, k):
+    rows, cols = shape
+    if cols < k:
+        pytest.skip("fewer columns than k")
+    say(f"topk {dtype} {shape} k={k}")
+    x = ref.lcg_f32(rows * cols, 1).reshape(rows, cols) * 4
+    if dtype == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+    xt = gpu(x, torch.float16 if dtype == "f16" else torch.float32)
+    got = host(rt.topk(xt, k))
+    want = ref.topk(x, k)
+    assert np.array_equal(got[:, :k], want[:, :k])
+    np.testing.assert_allclose(got[:, k:], want[:, k:], atol=1e-7, rtol=1e-5)
+
+
+def test_topk_ties_and_start_value(vectors):
+    say("topk ties")
+    v = vectors["topk_ties"]
+    got = host(rt.topk(gpu(np.array(v["x"], np.float32)), 4))
+    assert got[0, :4].tolist() == v["ids"][0]
+    assert got[1, :4].tolist() == v["ids"][1]
+    assert got[1, 4:].tolist() == v["weights_row1"]
+    v = vectors["topk_neg_inf"]
+    x = np.array([[float(a) for a in row] for row in v["x"]], np.float32)
+    assert host(rt.topk(gpu(x), 4)).tolist() == v["route"]
+
+
+def test_topk_k16_many_experts():
+    say("topk k=16 E=4096")
+    x = (ref.lcg_f32(33 * 4096, 3).reshape(33, 4096) * 8).round()  # many ties
+    got = host(rt.topk(gpu(x), 16))
+    want = ref.topk(x, 16)
+    assert np.array_equal(got[:, :16], want[:, :16])
+    np.testing.assert_allclose(got[:, 16:], want[:, 16:], atol=1e-7, rtol=1e-5)
+
+
+def test_topk_past_grid_stride():
+    # topkSelect.gpu.test.ts:74-84: GRID_Y_STRIDE + 5 rows of 4 columns.
+    rows = 65535 * 64 + 5
+    say(f"topk rows={rows}")
+    i = np.arange(rows * 4, dtype=np.int64)
+    x = (((i * 7) % 13) - (i % 4)).astype(np.float32).reshape(rows, 4)
+    got = host(rt.topk(gpu(x), 4))
+    want = ref.topk(x, 4)
+    assert np.array_equal(got[:, :4], want[:, :4])
+    np.testing.assert_allclose(got[:, 4:], want[:, 4:], atol=1e-7, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ router
+
+
+@pytest.mark.parametrize("T,d,E,k,dtype", [
+    (64, 512, 8, 2, "f32"), (1, 640, 128, 4, "f32"), (8, 2048, 64, 8, "f16"),
+    (300, 2048, 32, 4, "f16"), (257, 200, 128, 8, "f32"), (5, 64, 512, 16, "f32"),
+])
+def test_router_topk_bit_exact(T, d, E, k, dtype):
+    say(f"router T={T} d={d} E={E} k={k} {dtype}")
+    g = torch.Generator().manual_seed(T * 7 + E)
+    x = torch.randn((T, d), generator=g)
+    if dtype == "f16":
+        x = x.half()
+    w = torch.randn((d, E), generator=g) * 0.02
+    b = torch.randn((E,), generator=g) * 0.1
+    got = host(rt.router_topk(x.to(DEV), w.to(DEV), b.to(DEV), k))
+    logits = ref.router_logits(x.float().numpy(), w.numpy(), b.numpy())
+    want = ref.topk(logits, k)
+    assert np.array_equal(got[:, :k], want[:, :k]), "expert ids differ"
+    np.testing.assert_allclose(got[:, k:], want[:, k:], atol=1e-7, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- dispatch
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 4, 128), (8, 8, 64), (4096, 4, 32), (4096, 8, 128),
+                                   (1000, 3, 7), (2049, 2, 1024)])
+def test_dispatch_bit_exact(T, k, E):
+    say(f"dispatch T={T} k={k} E={E}")
+    rng = np.random.default_rng(T + k + E)
+    route = np.zeros((T, 2 * k), np.float32)
+    route[:, :k] = rng.integers(0, E, size=(T, k))
+    if T > 8:  # a few ids that are not experts
+        route[::97, 0] = -1
+        route[::101, k - 1] = E + 3
+        route[::103, 0] = 0.5
+    perm, offsets = rt.dispatch(gpu(route), E)
+    want_perm, _, want_off = ref.dispatch(route, E)
+    assert np.array_equal(host(offsets), want_off)
+    assert np.array_equal(host(perm), want_perm)
+
+
+# ---------------------------------------------------- expert products (ops)
+
+# The reference test's shapes (moeQuantW.gpu.test.ts:134-144) plus shapes
+# that take the MFMA path (groupSize K or a multiple of 32), with rows per
+# expert above 16, K tails and N not a multiple of 64.
+REF_SHAPES = [(1, 4, 8, 1, 4), (3, 16, 24, 4, 8), (2, 132, 8, 3, 4), (2, 64, 72, 5, 64),
+              (5, 32, 16, 8, 16)]
+MFMA_SHAPES = [(3, 64, 72, 5, 64), (40, 96, 136, 6, 32), (100, 100, 80, 3, 100),
+               (17, 2048, 1408, 4, 2048), (64, 512, 1024, 8, 512), (9, 640, 640, 16, 64)]
+
+
+def _check_up(T, K, N, E, g, bits, k=4, xdtype="f32", tol="ref"):
+    route = route_for(T, E, k)
+    glu, glu_h = weight_pair(E, K, N, bits, g, 10)
+    lin, lin_h = weight_pair(E, K, N, bits, g, 20)
+    x = (ref.lcg_f32(T * K, 1) * 4).reshape(T, K)
+    if xdtype == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+    xt = gpu(x, torch.float16 if xdtype == "f16" else torch.float32)
+    got = host(rt.moeUp(xt, gpu(route), glu, lin, {"bits": bits, "groupSize": g}))
+    want = ref.moe_up(x, route, glu_h, lin_h, bits, g, E)
+    if tol == "ref":
+        np.testing.assert_allclose(got, want, atol=1e-5 * K, rtol=1e-4)
+    assert_close(got, want, what="moeUp")
+
+
+def _check_down(T, K, N, E, g, bits, k=4):
+    route = route_for(T, E, k)
+    down, down_h = weight_pair(E, K, N, bits, g, 30)
+    act = ref.lcg_f32(T * k * K, 1).reshape(T * k, K)
+    res = ref.lcg_f32(T * N, 4).reshape(T, N)
+    got = host(rt.moeDown(gpu(act), gpu(route), down, gpu(res), {"bits": bits, "groupSize": g}))
+    want = ref.moe_down(act, route, down_h, res, bits, g, E)
+    np.testing.assert_allclose(got, want, atol=1e-5 * K, rtol=1e-4)
+    assert_close(got, want, what="moeDown")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("shape", REF_SHAPES)
+def test_moe_up_reference_shapes(bits, shape):
+    say(f"moeUp int{bits} {shape}")
+    T, K, N, E, g = shape
+    _check_up(T, K, N, E, g, bits)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("shape", REF_SHAPES)
+def test_moe_down_reference_shapes(bits, shape):
+    say(f"moeDown int{bits} {shape}")
+    T, K, N, E, g = shape
+    _check_down(T, K, N, E, g, bits)
+
+
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+@pytest.mark.parametrize("shape", MFMA_SHAPES)
+@pytest.mark.parametrize("k", [4, 2, 8])
+def test_moe_up_mfma(xdtype, shape, k):
+    T, K, N, E, g = shape
+    if E < k:
+        pytest.skip("fewer experts than k")
+    say(f"moeUp mfma {xdtype} {shape} k={k}")
+    _check_up(T, K, N, E, g, 8, k=k, xdtype=xdtype)
+
+
+@pytest.mark.parametrize("shape", MFMA_SHAPES)
+@pytest.mark.parametrize("k", [4, 8])
+def test_moe_down_mfma(shape, k):
+    T, K, N, E, g = shape
+    if E < k:
+        pytest.skip("fewer experts than k")
+    say(f"moeDown mfma {shape} k={k}")
+    _check_down(T, K, N, E, g, 8, k=k)
+
+
+def test_moe_up_past_65535_rows():
+    T = math.ceil(65535 / 4) + 1
+    say(f"moeUp rows={T * 4}")
+    _check_up(T, 4, 8, 2, 4, 8)
+
+
+def test_moe_down_past_65535_tokens():
+    T = 65535 + 2
+    say(f"moeDown tokens={T}")
+    _check_down(T, 4, 8, 2, 4, 8)
+
+
+def test_invalid_route_ids_give_zero_rows():
+    say("moeUp/moeDown invalid ids")
+    E, K, N = 3, 64, 64
+    glu, glu_h = weight_pair(E, K, N, 8, K, 10)
+    x = ref.lcg_f32(2 * K, 1).reshape(2, K)
+    route = np.array([[0, 7, 0.5, 0.5], [-1, 1.5, 0.5, 0.5]], np.float32)
+    got = host(rt.moeUp(gpu(x), gpu(route), glu, glu, {"bits": 8, "groupSize": K}))
+    want = ref.moe_up(x, route, glu_h, glu_h, 8, K, E)
+    assert not got[1:].any()
+    assert_close(got, want, what="moeUp")
+    out = host(rt.moeDown(gpu(got), gpu(route), glu, gpu(x), {"bits": 8, "groupSize": K}))
+    assert_close(out, ref.moe_down(want, route, glu_h, x, 8, K, E), what="moeDown")
+
+
+# ------------------------------------------------------------- the layer
+
+
+def _oracle_layer(inp, tokens):
+    """Oracle route and output for a subset of tokens (tokens are independent
+    in the layer, so a sample checks a full-size run)."""
+    cfg = inp.cfg
+    x = inp.x[tokens].float().cpu().numpy()
+    rw = inp.router_w.cpu().numpy()
+    rb = inp.router_b.cpu().numpy()
+    logits = ref.router_logits(x, rw, rb)
+    route = ref.topk(logits, cfg.k)
+    pk = {n: ref.pack_ekn(inp.q[n].numpy(), 8) for n in ("glu", "lin", "down")}
+    sc = {n: getattr(inp, n).scales.cpu().numpy() for n in ("glu", "lin", "down")}
+    bs = {n: getattr(inp, n).bias.cpu().numpy() for n in ("glu", "lin", "down")}
+    act = ref.moe_up(x, route, (pk["glu"], sc["glu"], bs["glu"]), (pk["lin"], sc["lin"], bs["lin"]),
+                     8, cfg.d, cfg.E)
+    res = inp.residual[tokens].cpu().numpy()
+    out = ref.moe_down(act, route, (pk["down"], sc["down"], bs["down"]), res, 8, cfg.I, cfg.E)
+    return route, out, logits
+
+
+@pytest.mark.parametrize("cid,sample", [(1, None), (2, None), (3, None), (4, 6), (5, 6)])
+def test_moe_layer_configs(cid, sample):
+    cfg = CONFIGS[cid]
+    say(f"moe_layer config {cid}: {cfg.name}")
+    inp = make_inputs(cfg, seed=cid, keep_q=True, bias_rand=True)
+    inp.residual.copy_(torch.randn_like(inp.residual))
+    out, route = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                              inp.residual, cfg.k, return_route=True)
+    got_out, got_route = host(out), host(route)
+    tokens = np.arange(cfg.T) if sample is None else np.linspace(0, cfg.T - 1, sample).astype(int)
+    want_route, want_out, logits = _oracle_layer(inp, tokens)
+    k = cfg.k
+    assert np.array_equal(got_route[tokens, :k], want_route[:, :k]), "expert ids differ"
+    np.testing.assert_allclose(got_route[tokens, k:], want_route[:, k:], atol=1e-7, rtol=1e-5)
+    assert_close(got_out[tokens], want_out, what=f"config {cid} output")
+    # every token routes to k distinct experts
+    ids = got_route[:, :k]
+    assert all(len(set(r)) == k for r in ids.tolist())
+
+
+def test_moe_layer_matches_ops():
+    """moe_layer = topk(router) → moeUp → moeDown composed from the ops."""
+    cfg = CONFIGS[1]
+    say("moe_layer vs ops")
+    inp = make_inputs(cfg, seed=11, bias_rand=True)
+    out, route = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                              inp.residual, cfg.k, return_route=True)
+    r2 = rt.router_topk(inp.x, inp.router_w, inp.router_b, cfg.k)
+    assert torch.equal(route, r2)
+    act = rt.moeUp(inp.x, r2, inp.glu, inp.lin, {"bits": 8, "groupSize": cfg.d})
+    o2 = rt.moeDown(act, r2, inp.down, inp.residual, {"bits": 8, "groupSize": cfg.I})
+    assert_close(host(out), host(o2), atol=1e-5, rtol=1e-5, what="layer vs ops")
