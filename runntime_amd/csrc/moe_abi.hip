@@ -110,9 +110,13 @@ extern "C" int moe_sync(moe_ctx *ctx) {
 
 static std::string S(long v) { return std::to_string(v); }
 
-static int check_k(const char *op, int k, int E) {
+// topk needs at least k columns; the expert ops take any route, including
+// one that names an expert twice (fewer experts than slots).
+static int check_k(const char *op, int k, int E, bool need_k_columns) {
   REQUIRE(k >= 1 && k <= MAX_K, std::string(op) + ": k must be in 1.." + S(MAX_K) + ", got " + S(k));
-  REQUIRE(E >= k, std::string(op) + ": need at least " + S(k) + " columns, got " + S(E));
+  if (need_k_columns)
+    REQUIRE(E >= k, std::string(op) + ": need at least " + S(k) + " columns, got " + S(E));
+  REQUIRE(E >= 1, std::string(op) + ": need at least one expert");
   return MOE_OK;
 }
 
@@ -191,7 +195,7 @@ extern "C" int moe_topk(moe_ctx *ctx, const void *logits, moe_dtype dtype, int T
                         float *route) {
   int rc = check_ctx(ctx, "topk");
   if (rc) return rc;
-  if ((rc = check_k("topk", k, E))) return rc;
+  if ((rc = check_k("topk", k, E, true))) return rc;
   REQUIRE(T >= 1, "topk: T must be at least 1, got " + S(T));
   REQUIRE(E <= TOPK_MAX_E, "topk: more than " + S(TOPK_MAX_E) + " columns");
   REQUIRE(logits && route, "topk: NULL tensor");
@@ -205,7 +209,7 @@ extern "C" int moe_router_topk(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
                                int k, float *route) {
   int rc = check_ctx(ctx, "router_topk");
   if (rc) return rc;
-  if ((rc = check_k("router_topk", k, E))) return rc;
+  if ((rc = check_k("router_topk", k, E, true))) return rc;
   REQUIRE(T >= 1 && d >= 1, "router_topk: T and d must be positive");
   REQUIRE(E <= ROUTER_MAX_E, "router_topk: more than " + S(ROUTER_MAX_E) + " experts");
   REQUIRE(x && w_router && route, "router_topk: NULL tensor");
@@ -223,7 +227,7 @@ extern "C" int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int 
                             int32_t *offsets) {
   int rc = check_ctx(ctx, "dispatch");
   if (rc) return rc;
-  if ((rc = check_k("dispatch", k, E))) return rc;
+  if ((rc = check_k("dispatch", k, E, false))) return rc;
   REQUIRE(T >= 1 && E <= 1024, "dispatch: T ≥ 1 and E ≤ 1024 required");
   LayerWs L;
   if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, 0, L))) return rc;
@@ -242,7 +246,7 @@ extern "C" int moe_up(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
                       int N, int E, int k, int bits, int group_size, float *act) {
   int rc = check_ctx(ctx, "moeUp");
   if (rc) return rc;
-  if ((rc = check_k("moeUp", k, E))) return rc;
+  if ((rc = check_k("moeUp", k, E, false))) return rc;
   if ((rc = check_weight("moeUp", glu, K, N, E, bits, group_size))) return rc;
   if ((rc = check_weight("moeUp", lin, K, N, E, bits, group_size))) return rc;
   REQUIRE(T >= 1, "moeUp: T must be at least 1");
@@ -263,7 +267,7 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
                         int E, int k, int bits, int group_size, float *out) {
   int rc = check_ctx(ctx, "moeDown");
   if (rc) return rc;
-  if ((rc = check_k("moeDown", k, E))) return rc;
+  if ((rc = check_k("moeDown", k, E, false))) return rc;
   if ((rc = check_weight("moeDown", down, K, N, E, bits, group_size))) return rc;
   REQUIRE(T >= 1, "moeDown: T must be at least 1");
   REQUIRE(act && route && out, "moeDown: NULL tensor");
@@ -284,7 +288,7 @@ extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const f
                          int group_size_up, int group_size_down, float *route_out, float *out) {
   int rc = check_ctx(ctx, "moe_layer");
   if (rc) return rc;
-  if ((rc = check_k("moe_layer", k, E))) return rc;
+  if ((rc = check_k("moe_layer", k, E, true))) return rc;
   if ((rc = check_weight("moe_layer", glu, d, I, E, bits, group_size_up))) return rc;
   if ((rc = check_weight("moe_layer", lin, d, I, E, bits, group_size_up))) return rc;
   if ((rc = check_weight("moe_layer", down, I, d, E, bits, group_size_down))) return rc;
