@@ -1,0 +1,290 @@
+"""MoE-layer throughput on one MI355X (BASELINE.json metric).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]
+
+Default workload: config 2 (the metric's decode configuration): 1000
+independent single-token layer calls (T=1, d=640, E=128, k=4, I=640, f32
+activations, int8 weights with per-channel scales). One step = the 1000
+calls, issued back to back on one stream and replayed from a HIP graph.
+Call j uses weight copy j mod C, so the expert weights (158 MB per copy) do
+not stay in the 256 MB MALL between calls. Inputs are resident in HBM
+before the timed region. Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import runntime_amd as rt  # noqa: E402
+from runntime_amd import perf  # noqa: E402
+from runntime_amd.synth import CONFIGS, make_inputs, make_weight_copies  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def say(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def layer_bytes(cfg, n_experts_active):
+    """Algorithmic HBM bytes of one layer call: the int8 weights and f32
+    scales of the active experts, the f32 router weight, x in and out."""
+    xb = 2 if cfg.x_dtype == "f16" else 4
+    per_expert = 3 * cfg.d * cfg.I + 2 * cfg.I * 4 + cfg.d * 4
+    return (n_experts_active * per_expert + cfg.d * cfg.E * 4 + cfg.T * cfg.d * (xb + 4))
+
+
+def up_kernel_bytes(cfg, n_experts_active):
+    """Algorithmic bytes of one gate/up launch: glu+lin int8 weights and
+    scales of the active experts, the x rows it reads, the act rows it
+    writes."""
+    xb = 2 if cfg.x_dtype == "f16" else 4
+    return (n_experts_active * (2 * cfg.d * cfg.I + 2 * cfg.I * 4)
+            + cfg.T * cfg.d * xb + cfg.T * cfg.k * cfg.I * 4)
+
+
+def layer_flops(cfg):
+    return 2 * cfg.T * cfg.d * cfg.E + cfg.T * cfg.k * 6 * cfg.d * cfg.I
+
+
+def cpu_baseline(cfg, seconds_budget=15.0):
+    """The oracle's f32 restatement of the reference's WGSL kernels
+    (topkSelect, moeUp, moeDown; router in the canonical f32 order), timed
+    on this host's cores on a bounded sample of the same workload."""
+    from oracle import ref
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    inp = make_inputs(cfg, seed=1234, device="cpu", keep_q=True, T=64 if cfg.T == 1 else cfg.T)
+    x = inp.x.float().numpy()
+    pk = {n: (ref.pack_ekn(inp.q[n].numpy(), 8), getattr(inp, n).scales.numpy(),
+              getattr(inp, n).bias.numpy()) for n in ("glu", "lin", "down")}
+    rw, rb = inp.router_w.numpy(), inp.router_b.numpy()
+    tokens = 0
+    t0 = time.perf_counter()
+    # single-token calls for the decode config, as the GPU runs them
+    step_T = 1 if cfg.T == 1 else min(cfg.T, 64)
+    i = 0
+    while time.perf_counter() - t0 < seconds_budget:
+        xs = x[i % len(x):i % len(x) + step_T] if step_T == 1 else x[:step_T]
+        route = ref.topk(ref.router_logits(xs, rw, rb), cfg.k)
+        act = ref.moe_up(xs, route, pk["glu"], pk["lin"], 8, cfg.d, cfg.E, f32ref=True)
+        ref.moe_down(act, route, pk["down"], None, 8, cfg.I, cfg.E, f32ref=True)
+        tokens += step_T
+        i += 1
+    dt = time.perf_counter() - t0
+    return {"value": tokens / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{tokens} tokens of {cfg.name} in {step_T}-token calls, {dt:.1f} s; "
+                      "oracle/moe_oracle.c f32 restatement of topkSelect/moeUp/moeDown "
+                      "(32-lane K split, fixed tree merge), OpenMP over rows"}
+
+
+def bench_decode(cfg, args):
+    """config 2: 1000 independent single-token calls per step. Each launch of
+    moe_layer_batched runs W of them; call j uses weight copy j mod W, so no
+    two calls in flight share a byte of weights and every copy is read again
+    only after W·158 MB of other traffic (the 256 MB MALL cannot hold it)."""
+    n_tok = cfg.tokens
+    W = args.calls_per_launch
+    say(f"drawing {W} weight copies of {cfg.name} on the GPU")
+    wc = make_weight_copies(cfg, W, seed=100, device="cuda")
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn((n_tok, 1, cfg.d), generator=g).to("cuda")
+    residual = torch.zeros((n_tok, 1, cfg.d), dtype=torch.float32, device="cuda")
+    out = torch.empty((n_tok, 1, cfg.d), dtype=torch.float32, device="cuda")
+    routes = torch.empty((n_tok, 1, 2 * cfg.k), dtype=torch.float32, device="cuda")
+    perf.reserve_batched(W, 1, cfg.d, cfg.I, cfg.E, cfg.k)
+
+    def step():
+        for j0 in range(0, n_tok, W):
+            n = min(W, n_tok - j0)
+            rt.moe_layer_batched(
+                x[j0:j0 + n], wc.router_w[:n], wc.router_b[:n],
+                rt.QuantExpertWeight(rt.QuantW(wc.glu.w.words[:n], wc.glu.w.dims), wc.glu.scales[:n], wc.glu.bias[:n]),
+                rt.QuantExpertWeight(rt.QuantW(wc.lin.w.words[:n], wc.lin.w.dims), wc.lin.scales[:n], wc.lin.bias[:n]),
+                rt.QuantExpertWeight(rt.QuantW(wc.down.w.words[:n], wc.down.w.dims), wc.down.scales[:n], wc.down.bias[:n]),
+                residual[j0:j0 + n], cfg.k, out=out[j0:j0 + n], route=routes[j0:j0 + n])
+
+    return step, n_tok
+
+
+def sequential_rate(cfg, args):
+    """The launch-bound case: the 1000 calls one at a time (W = 1), replayed
+    from a graph. Reported beside the main figure."""
+    wc = make_weight_copies(cfg, 4, seed=300, device="cuda")
+    g = torch.Generator().manual_seed(9)
+    n_tok = cfg.tokens
+    x = torch.randn((n_tok, 1, cfg.d), generator=g).to("cuda")
+    out = torch.empty((n_tok, 1, cfg.d), dtype=torch.float32, device="cuda")
+    routes = torch.empty((n_tok, 1, 2 * cfg.k), dtype=torch.float32, device="cuda")
+    perf.reserve_batched(1, 1, cfg.d, cfg.I, cfg.E, cfg.k)
+
+    def step():
+        for j in range(n_tok):
+            c = j % 4
+            rt.moe_layer_batched(
+                x[j:j + 1], wc.router_w[c:c + 1], wc.router_b[c:c + 1],
+                rt.QuantExpertWeight(rt.QuantW(wc.glu.w.words[c:c + 1], wc.glu.w.dims), wc.glu.scales[c:c + 1], wc.glu.bias[c:c + 1]),
+                rt.QuantExpertWeight(rt.QuantW(wc.lin.w.words[c:c + 1], wc.lin.w.dims), wc.lin.scales[c:c + 1], wc.lin.bias[c:c + 1]),
+                rt.QuantExpertWeight(rt.QuantW(wc.down.w.words[c:c + 1], wc.down.w.dims), wc.down.scales[c:c + 1], wc.down.bias[c:c + 1]),
+                None, cfg.k, out=out[j:j + 1], route=routes[j:j + 1])
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 3
+    del wc, graph
+    torch.cuda.empty_cache()
+    return n_tok / dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--copies", type=int, default=2, help="rotating input sets (config 3)")
+    ap.add_argument("--calls-per-launch", type=int, default=100,
+                    help="config 2: independent single-token calls per batched launch")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sequential", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    cfg = CONFIGS[args.config]
+
+    if args.config == 2:
+        step, tokens_per_step = bench_decode(cfg, args)
+    else:
+        C = args.copies if args.config == 3 else 1
+        say(f"building {C} input set(s) of {cfg.name}")
+        sets = [make_inputs(cfg, seed=200 + c, device="cuda") for c in range(C)]
+        out = torch.empty((cfg.T, cfg.d), dtype=torch.float32, device="cuda")
+        perf.reserve(cfg.T, cfg.d, cfg.I, cfg.E, cfg.k)
+        counter = [0]
+
+        def step():
+            for c in range(C):
+                w = sets[c]
+                o = rt.moe_layer(w.x, w.router_w, w.router_b, w.glu, w.lin, w.down, w.residual,
+                                 cfg.k)
+                out.copy_(o)
+        tokens_per_step = cfg.T * C
+
+    stream = torch.cuda.Stream()
+    graph = None
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        if not args.no_graph:
+            say("capturing graph")
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                step()
+            torch.cuda.synchronize()
+            for _ in range(args.warmup):
+                graph.replay()
+        torch.cuda.synchronize()
+
+        say(f"timing {args.steps} steps")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            if graph is not None:
+                graph.replay()
+            else:
+                step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+
+        # Per-kernel durations: one more eager step with the event sink on.
+        perf.read(reset=True)
+        perf.enable(True)
+        step()
+        torch.cuda.synchronize()
+        groups = perf.read(reset=True)
+        perf.enable(False)
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = tokens_per_step * args.steps / elapsed
+
+    # Experts touched per call: every token routes to k distinct experts.
+    if args.config == 2:
+        active_per_call = cfg.k
+        calls = tokens_per_step
+        W = args.calls_per_launch
+    else:
+        active_per_call = min(cfg.E, cfg.T * cfg.k)
+        calls = tokens_per_step // cfg.T
+    up_ms, up_n = groups.get("up", (0.0, 0))
+    up_avg_s = up_ms / max(up_n, 1) / 1e3
+    if args.config in (2, 3):
+        per_launch = up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1)
+        achieved = per_launch / up_avg_s / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "k_expert_skinny<up> (gate/up + SwiGLU)",
+                    "algorithmic_bytes_per_launch": per_launch,
+                    "avg_launch_us": round(up_avg_s * 1e6, 2)}
+        layer_frac = layer_bytes(cfg, active_per_call) * calls / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS
+    else:
+        fl = cfg.T * cfg.k * 4 * cfg.d * cfg.I
+        achieved = fl / up_avg_s / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                    "traffic": None, "kernel": "gate/up grouped GEMM",
+                    "algorithmic_flops_per_launch": fl, "avg_launch_us": round(up_avg_s * 1e6, 2)}
+        layer_frac = layer_flops(cfg) * calls / (ms_per_step / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS
+
+    line = {
+        "metric": "MoE-layer tokens/s at 1 MI355X",
+        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded; int8 weights U[-127,127], scales U(0.5e-3,2e-3), x~N(0,1))",
+        "config": {"workload": cfg.name, "T": cfg.T, "d": cfg.d, "E": cfg.E, "k": cfg.k,
+                   "I": cfg.I, "x_dtype": cfg.x_dtype, "tokens_per_step": tokens_per_step,
+                   "calls_per_step": calls,
+                   "calls_per_launch": args.calls_per_launch if args.config == 2 else 1,
+                   "weight_copies": (args.calls_per_launch if args.config == 2
+                                     else args.copies if args.config == 3 else 1),
+                   "graph": graph is not None, "parallelism": "single GPU",
+                   "arith": "int8 weights exact in f16 MFMA, f32 inputs split hi+lo, f32 accumulate"},
+        "layer_roofline_frac": round(layer_frac, 4),
+        "kernel_ms": {g: round(ms / n, 5) for g, (ms, n) in groups.items()},
+        "roofline": roofline,
+    }
+    if args.config == 2 and not args.no_sequential:
+        say("sequential (launch-bound) rate")
+        line["sequential_tokens_per_s"] = round(sequential_rate(cfg, args), 1)
+    if not args.no_cpu_baseline:
+        say("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -93,6 +93,8 @@ MOE_API int moe_ctx_set_stream(moe_ctx *ctx, void *stream);
 /* Grow the workspace now for layers up to these sizes, so later calls with
  * no larger shapes allocate nothing. */
 MOE_API int moe_ctx_reserve(moe_ctx *ctx, int T, int d, int I, int E, int k);
+/* As moe_ctx_reserve, for moe_layer_batched with up to `calls` calls. */
+MOE_API int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, int I, int E, int k);
 MOE_API int moe_ctx_destroy(moe_ctx *ctx);
 /* Wait for the context's stream; reports a device fault as EXECUTION_FAILED. */
 MOE_API int moe_sync(moe_ctx *ctx);
@@ -135,6 +137,42 @@ MOE_API int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
               const moe_expert_weight *down, const float *residual, int T, int d, int I, int E,
               int k, int bits, int group_size_up, int group_size_down, float *route_out,
               float *out);
+
+/* Strides between the calls of moe_layer_batched, in elements of each
+ * tensor (u32 words for quantW weights). 0 shares a tensor between calls. */
+typedef struct moe_call_strides {
+  int64_t x, router_w, router_b;
+  int64_t glu_w, glu_scales, glu_bias;
+  int64_t lin_w, lin_scales, lin_bias;
+  int64_t down_w, down_scales, down_bias;
+  int64_t residual, route, out;
+} moe_call_strides;
+
+/* `calls` independent moe_layer calls of identical shape, enqueued as one
+ * set of kernels: call c reads and writes every tensor at
+ * base + c·stride (strides NULL: all 0, valid for calls == 1). Each call is
+ * routed, dispatched and computed on its own, exactly as moe_layer would;
+ * the calls only share the launches. x, out and route_out need non-zero
+ * strides when calls > 1. No reference counterpart: it lets single-token
+ * decode calls of separate layer instances (e.g. independent requests on
+ * separate weight sets) fill the GPU instead of running one launch-bound
+ * call at a time. */
+MOE_API int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides *strides,
+                              const void *x, moe_dtype x_dtype, const float *w_router,
+                              const float *b_router, const moe_expert_weight *glu,
+                              const moe_expert_weight *lin, const moe_expert_weight *down,
+                              const float *residual, int T, int d, int I, int E, int k, int bits,
+                              int group_size_up, int group_size_down, float *route_out,
+                              float *out);
+
+/* Per-kernel-group timing on the context's stream — the reference's
+ * GpuPerfSink with perOp (src/core/gpu/perf.ts:1-23, timing.ts:62-111).
+ * While enabled, every launch group is bracketed by a HIP event pair.
+ * moe_prof_read waits for the stream and returns, per group (index: 0 topk,
+ * 1 router, 2 dispatch, 3 up, 4 down, 5 combine; 8 slots), the summed
+ * milliseconds and the number of timed groups; reset != 0 clears them. */
+MOE_API int moe_prof_enable(moe_ctx *ctx, int on);
+MOE_API int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *count_out);
 
 /* Test and diagnostic hook: the dispatch permutation of a route, as the
  * layer builds it. perm [T·k] (sorted position → assignment t·k + s, −1

@@ -314,68 +314,72 @@ static void merge_lanes(float p[K_LANES][4]) {
       for (int c = 0; c < 4; c++) p[l][c] = p[l][c] + p[l + stride][c];
 }
 
-/* moeUpKernel (moeQuantW.ts:122-175) in f32, rows in parallel. */
+/* moeUpKernel (moeQuantW.ts:122-175) in f32. Like the reference's grid, every
+ * (row, 4-column unit) is independent: they run in parallel. */
 EXPORT void orc_moe_up_f32ref(const float *x, const float *route, const uint32_t *glu_w,
                               const float *glu_s, const float *glu_b, const uint32_t *lin_w,
                               const float *lin_s, const float *lin_b, int T, int K, int N, int E,
                               int k, int bits, int g, float *act) {
   int64_t rows = (int64_t)T * k;
-#pragma omp parallel for schedule(dynamic, 4)
-  for (int64_t row = 0; row < rows; row++) {
+  int n4 = N / 4;
+#pragma omp parallel for schedule(dynamic, 8)
+  for (int64_t ru = 0; ru < rows * n4; ru++) {
+    int64_t row = ru / n4;
+    int unit = (int)(ru % n4);
     int t = (int)(row / k), s = (int)(row % k);
     float *arow = act + row * N;
     int e = route_id(route, t, k, s, E);
-    if (e < 0) { memset(arow, 0, sizeof(float) * N); continue; }
+    if (e < 0) { for (int c = 0; c < 4; c++) arow[unit * 4 + c] = 0.0f; continue; }
     float pa[K_LANES][4], pb[K_LANES][4];
-    for (int unit = 0; unit < N / 4; unit++) {
-      for (int lane = 0; lane < K_LANES; lane++) {
-        lane_dots(x + (int64_t)t * K, glu_w, glu_s, K, N, bits, g, e, unit, lane, pa[lane]);
-        lane_dots(x + (int64_t)t * K, lin_w, lin_s, K, N, bits, g, e, unit, lane, pb[lane]);
-      }
-      merge_lanes(pa);
-      merge_lanes(pb);
-      for (int c = 0; c < 4; c++) {
-        int n = unit * 4 + c;
-        float gb = glu_b ? glu_b[(int64_t)e * N + n] : 0.0f;
-        float lb = lin_b ? lin_b[(int64_t)e * N + n] : 0.0f;
-        arow[n] = swiglu_f32(pa[0][c] + gb, pb[0][c] + lb);
-      }
+    for (int lane = 0; lane < K_LANES; lane++) {
+      lane_dots(x + (int64_t)t * K, glu_w, glu_s, K, N, bits, g, e, unit, lane, pa[lane]);
+      lane_dots(x + (int64_t)t * K, lin_w, lin_s, K, N, bits, g, e, unit, lane, pb[lane]);
+    }
+    merge_lanes(pa);
+    merge_lanes(pb);
+    for (int c = 0; c < 4; c++) {
+      int n = unit * 4 + c;
+      float gb = glu_b ? glu_b[(int64_t)e * N + n] : 0.0f;
+      float lb = lin_b ? lin_b[(int64_t)e * N + n] : 0.0f;
+      arow[n] = swiglu_f32(pa[0][c] + gb, pb[0][c] + lb);
     }
   }
 }
 
 /* moeDownKernel (moeQuantW.ts:188-237) in f32: per slot a K-split dot scaled
- * by its gate, lanes merged, then residual and the gate-weighted biases. */
+ * by its gate, lanes merged, then residual and the gate-weighted biases.
+ * Every (token, unit) is independent: they run in parallel. */
 EXPORT void orc_moe_down_f32ref(const float *act, const float *route, const uint32_t *w,
                                 const float *sc, const float *bias, const float *residual, int T,
                                 int K, int N, int E, int k, int bits, int g, float *out) {
-#pragma omp parallel for schedule(dynamic, 1)
-  for (int t = 0; t < T; t++) {
+  int n4 = N / 4;
+#pragma omp parallel for schedule(dynamic, 8)
+  for (int64_t tu = 0; tu < (int64_t)T * n4; tu++) {
+    int t = (int)(tu / n4);
+    int unit = (int)(tu % n4);
     float p[K_LANES][4];
-    for (int unit = 0; unit < N / 4; unit++) {
-      for (int lane = 0; lane < K_LANES; lane++) {
-        float acc[4] = {0, 0, 0, 0};
-        for (int s = 0; s < k; s++) {
-          int e = route_id(route, t, k, s, E);
-          if (e < 0) continue;
-          float gate = route[(int64_t)t * 2 * k + k + s];
-          float dot[4];
-          lane_dots(act + ((int64_t)t * k + s) * K, w, sc, K, N, bits, g, e, unit, lane, dot);
-          for (int c = 0; c < 4; c++) acc[c] += dot[c] * gate;
-        }
-        for (int c = 0; c < 4; c++) p[lane][c] = acc[c];
+    for (int lane = 0; lane < K_LANES; lane++) {
+      float acc[4] = {0, 0, 0, 0};
+      for (int s = 0; s < k; s++) {
+        int e = route_id(route, t, k, s, E);
+        if (e < 0) continue;
+        float gate = route[(int64_t)t * 2 * k + k + s];
+        float dot[4];
+        lane_dots(act + ((int64_t)t * k + s) * K, w, sc, K, N, bits, g, e, unit, lane, dot);
+        for (int c = 0; c < 4; c++) acc[c] += dot[c] * gate;
       }
-      merge_lanes(p);
-      for (int c = 0; c < 4; c++) {
-        int n = unit * 4 + c;
-        float sum = p[0][c] + (residual ? residual[(int64_t)t * N + n] : 0.0f);
-        for (int s = 0; s < k; s++) {
-          int e = route_id(route, t, k, s, E);
-          if (e < 0 || !bias) continue;
-          sum += bias[(int64_t)e * N + n] * route[(int64_t)t * 2 * k + k + s];
-        }
-        out[(int64_t)t * N + n] = sum;
+      for (int c = 0; c < 4; c++) p[lane][c] = acc[c];
+    }
+    merge_lanes(p);
+    for (int c = 0; c < 4; c++) {
+      int n = unit * 4 + c;
+      float sum = p[0][c] + (residual ? residual[(int64_t)t * N + n] : 0.0f);
+      for (int s = 0; s < k; s++) {
+        int e = route_id(route, t, k, s, E);
+        if (e < 0 || !bias) continue;
+        sum += bias[(int64_t)e * N + n] * route[(int64_t)t * 2 * k + k + s];
       }
+      out[(int64_t)t * N + n] = sum;
     }
   }
 }

@@ -18,8 +18,17 @@ MOE_F16 = 1
 EXPORTED = (
     "moe_version", "moe_last_error", "moe_ctx_create", "moe_ctx_set_stream",
     "moe_ctx_reserve", "moe_ctx_destroy", "moe_sync", "moe_topk", "moe_router_topk",
-    "moe_up", "moe_down", "moe_layer", "moe_dispatch",
+    "moe_up", "moe_down", "moe_layer", "moe_dispatch", "moe_prof_enable", "moe_prof_read",
+    "moe_layer_batched", "moe_ctx_reserve_batched",
 )
+PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine")
+
+
+class CallStridesC(ctypes.Structure):
+    """moe_call_strides: element strides between the calls of a batch."""
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "x", "router_w", "router_b", "glu_w", "glu_scales", "glu_bias", "lin_w", "lin_scales",
+        "lin_bias", "down_w", "down_scales", "down_bias", "residual", "route", "out")]
 
 
 class ExpertWeightC(ctypes.Structure):
@@ -59,6 +68,11 @@ def load() -> ctypes.CDLL:
             "moe_down": ([P, P, P, W, P, I, I, I, I, I, I, I, P], I),
             "moe_layer": ([P, P, I, P, P, W, W, W, P, I, I, I, I, I, I, I, I, P, P], I),
             "moe_dispatch": ([P, P, I, I, I, P, P], I),
+            "moe_prof_enable": ([P, I], I),
+            "moe_layer_batched": ([P, I, ctypes.POINTER(CallStridesC), P, I, P, P, W, W, W, P, I,
+                                   I, I, I, I, I, I, I, P, P], I),
+            "moe_ctx_reserve_batched": ([P, I, I, I, I, I, I], I),
+            "moe_prof_read": ([P, I, P, P], I),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)

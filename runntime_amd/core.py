@@ -264,3 +264,59 @@ def dispatch(route, num_experts: int):
     _lib.check(lib.moe_dispatch(_ctx(dev), route.data_ptr(), t, num_experts, k, perm.data_ptr(),
                                 offsets.data_ptr()))
     return perm, offsets
+
+
+def _call_stride(t, calls: int, base_dims: int) -> int:
+    """Element stride between calls: a tensor with one more leading dim than
+    `base_dims` is per call (its leading size must be `calls`), else shared."""
+    if t is None:
+        return 0
+    tt = t.words if isinstance(t, QuantW) else t
+    if tt.dim() == base_dims + 1:
+        if tt.shape[0] != calls:
+            raise ValueError(f"moe_layer_batched: leading dim {tt.shape[0]} != calls {calls}")
+        return tt.stride(0)
+    if tt.dim() != base_dims:
+        raise ValueError(f"moe_layer_batched: expected {base_dims} or {base_dims + 1} dims, "
+                         f"got {tt.dim()}")
+    return 0
+
+
+def moe_layer_batched(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWeight,
+                      down: QuantExpertWeight, residual, k: int, bits: int = 8,
+                      group_size_up=None, group_size_down=None, out=None, route=None):
+    """`calls` independent moe_layer calls in one set of launches
+    (moe_layer_batched in include/runntime_moe.h). x is [calls, T, d]; every
+    other tensor is either per call (a leading `calls` dim) or shared. The
+    quantW words of a per-call weight are [calls, words]. Returns
+    (out [calls, T, d], route [calls, T, 2k])."""
+    if x.dim() != 3:
+        raise ValueError("moe_layer_batched: x must be [calls, T, d]")
+    calls, t, d = x.shape
+    rw = router_w.shape
+    e = rw[-1]
+    i = glu.w.dims[1]
+    gu = group_size_up or d
+    gd = group_size_down or i
+    dev = _device_of(x, router_w, router_b, glu.w, glu.scales, lin.w, down.w, residual)
+    if out is None:
+        out = torch.empty((calls, t, d), dtype=torch.float32, device=dev)
+    if route is None:
+        route = torch.empty((calls, t, 2 * k), dtype=torch.float32, device=dev)
+    st = _lib.CallStridesC(
+        x=x.stride(0), router_w=_call_stride(router_w, calls, 2),
+        router_b=_call_stride(router_b, calls, 1),
+        glu_w=_call_stride(glu.w, calls, 1), glu_scales=_call_stride(glu.scales, calls, 2),
+        glu_bias=_call_stride(glu.bias, calls, 2),
+        lin_w=_call_stride(lin.w, calls, 1), lin_scales=_call_stride(lin.scales, calls, 2),
+        lin_bias=_call_stride(lin.bias, calls, 2),
+        down_w=_call_stride(down.w, calls, 1), down_scales=_call_stride(down.scales, calls, 2),
+        down_bias=_call_stride(down.bias, calls, 2),
+        residual=_call_stride(residual, calls, 2), route=route.stride(0), out=out.stride(0))
+    g, l_, dn = _weight_c(glu), _weight_c(lin), _weight_c(down)
+    lib = _lib.load()
+    _lib.check(lib.moe_layer_batched(
+        _ctx(dev), calls, ctypes.byref(st), x.data_ptr(), _xdtype(x), router_w.data_ptr(),
+        _ptr(router_b), ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn), _ptr(residual), t, d,
+        i, e, k, bits, gu, gd, route.data_ptr(), out.data_ptr()))
+    return out, route

@@ -35,8 +35,10 @@ constexpr int WAVE = 64;
 
 struct ExpertKArgs {
   const void *a;
+  int64_t a_cs;
   int a_row_div;
   const float *route;
+  int64_t route_cs;
   int k;
   const uint32_t *w0;
   const float *s0;
@@ -44,12 +46,11 @@ struct ExpertKArgs {
   const uint32_t *w1;
   const float *s1;
   const float *b1;
+  int64_t w0_cs, s0_cs, b0_cs, w1_cs, s1_cs, b1_cs;
   int K, N, E, bits, g;
   float *out;
-  const int32_t *perm;
-  const int32_t *offsets;
-  const int32_t *active;
-  const int32_t *meta;
+  int64_t out_cs;
+  DispatchBufs db;
 };
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
@@ -123,16 +124,32 @@ struct AFrag<float> {
   }
 };
 
+template <int NARR>
+struct WTiles {
+  uint4 t0[NARR], t1[NARR];
+};
+
 template <int MODE, typename AT>
 __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
   constexpr int NARR = (MODE == MODE_UP) ? 2 : 1;
   __shared__ floatx4 red[4][NARR * 4][WAVE];
 
-  int slot = blockIdx.y;
-  if (slot >= p.meta[META_ACTIVE]) return;
-  const int e = p.active[slot];
-  const int p0 = p.offsets[e];
-  const int cnt = p.offsets[e + 1] - p0;
+  const int call = blockIdx.z;
+  const int32_t *meta = p.db.meta + call * p.db.meta_cs();
+  const int slot = blockIdx.y;
+  if (slot >= meta[META_ACTIVE]) return;
+  const int e = p.db.active[call * p.db.act_cs() + slot];
+  const int32_t *offsets = p.db.offsets + call * p.db.off_cs();
+  const int32_t *perm = p.db.perm + call * p.db.perm_cs();
+  const int p0 = offsets[e];
+  const int cnt = offsets[e + 1] - p0;
+  const void *abase = (const char *)p.a + call * p.a_cs * (int64_t)sizeof(AT);
+  float *out = p.out + call * p.out_cs;
+  const float *s0 = p.s0 + call * p.s0_cs;
+  const float *s1 = (NARR == 2) ? p.s1 + call * p.s1_cs : nullptr;
+  const float *b0 = p.b0 ? p.b0 + call * p.b0_cs : nullptr;
+  const float *b1 = (NARR == 2 && p.b1) ? p.b1 + call * p.b1_cs : nullptr;
+
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int N4 = p.N / 4, K4 = p.K / 4;
@@ -145,15 +162,25 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
   const int se = min(steps, sb + per);
   const int kg = p.K / p.g;
 
-  const uint4 *wt0 = (const uint4 *)p.w0 + ((int64_t)e * N4 + (uok ? u : 0)) * K4;
-  const uint4 *wt1 = (NARR == 2) ? (const uint4 *)p.w1 + ((int64_t)e * N4 + (uok ? u : 0)) * K4
-                                 : nullptr;
+  const uint4 *wt[2];
+  wt[0] = (const uint4 *)(p.w0 + call * p.w0_cs) + ((int64_t)e * N4 + (uok ? u : 0)) * K4;
+  wt[1] = (NARR == 2) ? (const uint4 *)(p.w1 + call * p.w1_cs) + ((int64_t)e * N4 + (uok ? u : 0)) * K4
+                      : nullptr;
+
+  auto load_w = [&](int step, WTiles<NARR> &w) {
+    const int k4 = step * 8 + kq * 2;
+#pragma unroll
+    for (int a = 0; a < NARR; a++) {
+      w.t0[a] = (uok && k4 < K4) ? wt[a][k4] : uint4{0, 0, 0, 0};
+      w.t1[a] = (uok && k4 + 1 < K4) ? wt[a][k4 + 1] : uint4{0, 0, 0, 0};
+    }
+  };
 
   for (int c0 = 0; c0 < cnt; c0 += 16) {
     const int m = lane & 15;
     const bool rvalid = c0 + m < cnt;
     int64_t src_row = 0;
-    if (rvalid) src_row = p.perm[p0 + c0 + m] / p.a_row_div;
+    if (rvalid) src_row = perm[p0 + c0 + m] / p.a_row_div;
 
     floatx4 tot[NARR][4], tmp[NARR][4];
 #pragma unroll
@@ -164,33 +191,31 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
         tmp[a][i] = floatx4{0.f, 0.f, 0.f, 0.f};
       }
 
+    // Double-buffered: the next step's weight tiles are in flight while the
+    // current step's MFMAs run.
+    WTiles<NARR> cur, nxt;
+    if (sb < se) load_w(sb, nxt);
     for (int step = sb; step < se; step++) {
+      cur = nxt;
+      if (step + 1 < se) load_w(step + 1, nxt);
       const int k0 = step * 32 + kq * 8;
       half8 ahi, alo;
-      AFrag<AT>::load(p.a, src_row, p.K, k0, rvalid, ahi, alo);
-      const int k4 = step * 8 + kq * 2;
-      uint4 t0[NARR], t1[NARR];
+      AFrag<AT>::load(abase, src_row, p.K, k0, rvalid, ahi, alo);
 #pragma unroll
       for (int a = 0; a < NARR; a++) {
-        const uint4 *wt = (a == 0) ? wt0 : wt1;
-        t0[a] = (uok && k4 < K4) ? wt[k4] : uint4{0, 0, 0, 0};
-        t1[a] = (uok && k4 + 1 < K4) ? wt[k4 + 1] : uint4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int a = 0; a < NARR; a++) {
-        half8 b0 = cvt_i8x8(t0[a].x, t1[a].x);
-        half8 b1 = cvt_i8x8(t0[a].y, t1[a].y);
-        half8 b2 = cvt_i8x8(t0[a].z, t1[a].z);
-        half8 b3 = cvt_i8x8(t0[a].w, t1[a].w);
-        tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b0, tmp[a][0], 0, 0, 0);
-        tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b1, tmp[a][1], 0, 0, 0);
-        tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b2, tmp[a][2], 0, 0, 0);
-        tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b3, tmp[a][3], 0, 0, 0);
+        half8 b0v = cvt_i8x8(cur.t0[a].x, cur.t1[a].x);
+        half8 b1v = cvt_i8x8(cur.t0[a].y, cur.t1[a].y);
+        half8 b2v = cvt_i8x8(cur.t0[a].z, cur.t1[a].z);
+        half8 b3v = cvt_i8x8(cur.t0[a].w, cur.t1[a].w);
+        tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b0v, tmp[a][0], 0, 0, 0);
+        tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b1v, tmp[a][1], 0, 0, 0);
+        tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b2v, tmp[a][2], 0, 0, 0);
+        tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b3v, tmp[a][3], 0, 0, 0);
         if (AFrag<AT>::SPLIT) {
-          tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b0, tmp[a][0], 0, 0, 0);
-          tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b1, tmp[a][1], 0, 0, 0);
-          tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b2, tmp[a][2], 0, 0, 0);
-          tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b3, tmp[a][3], 0, 0, 0);
+          tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b0v, tmp[a][0], 0, 0, 0);
+          tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b1v, tmp[a][1], 0, 0, 0);
+          tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b2v, tmp[a][2], 0, 0, 0);
+          tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b3v, tmp[a][3], 0, 0, 0);
         }
       }
       // Fold the group's partial sums with its scales at each group end and
@@ -200,7 +225,7 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
         const int grp = (step * 32) / p.g;
 #pragma unroll
         for (int a = 0; a < NARR; a++) {
-          const float *sc = (a == 0) ? p.s0 : p.s1;
+          const float *sc = (a == 0) ? s0 : s1;
           floatx4 s4 = uok ? *(const floatx4 *)(sc + ((int64_t)e * kg + grp) * p.N + 4 * u)
                            : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -232,19 +257,19 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
       }
       if (uok) {
         const int n = 4 * u + i;
-        const float bias0 = p.b0 ? p.b0[(int64_t)e * p.N + n] : 0.f;
-        const float bias1 = (NARR == 2 && p.b1) ? p.b1[(int64_t)e * p.N + n] : 0.f;
+        const float bias0 = b0 ? b0[(int64_t)e * p.N + n] : 0.f;
+        const float bias1 = b1 ? b1[(int64_t)e * p.N + n] : 0.f;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const int mm = kq * 4 + q;
           if (c0 + mm < cnt) {
-            const int64_t asg = p.perm[p0 + c0 + mm];
+            const int64_t asg = perm[p0 + c0 + mm];
             float v;
             if (MODE == MODE_UP)
               v = swiglu(sum[0][q] + bias0, sum[NARR - 1][q] + bias1);
             else
               v = sum[0][q] + bias0;
-            p.out[asg * p.N + n] = v;
+            out[asg * p.N + n] = v;
           }
         }
       }
@@ -274,19 +299,20 @@ __device__ __forceinline__ float qval(const uint32_t *w, int K, int N, int bits,
 
 template <int MODE, typename AT>
 __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
+  const int call = blockIdx.z;
   const int pos = blockIdx.x;
-  if (pos >= p.meta[META_VALID]) return;
+  if (pos >= p.db.meta[call * p.db.meta_cs() + META_VALID]) return;
   const int n = blockIdx.y * 256 + threadIdx.x;
   if (n >= p.N) return;
-  const int64_t asg = p.perm[pos];
-  const int e = route_expert(p.route, asg, p.k, p.E);
-  const AT *x = (const AT *)p.a + (asg / p.a_row_div) * p.K;
+  const int64_t asg = p.db.perm[call * p.db.perm_cs() + pos];
+  const int e = route_expert(p.route + call * p.route_cs, asg, p.k, p.E);
+  const AT *x = (const AT *)p.a + call * p.a_cs + (asg / p.a_row_div) * p.K;
   const int kg = p.K / p.g;
   float acc[2] = {0.f, 0.f};
   constexpr int NARR = (MODE == MODE_UP) ? 2 : 1;
   for (int a = 0; a < NARR; a++) {
-    const uint32_t *w = a == 0 ? p.w0 : p.w1;
-    const float *sc = a == 0 ? p.s0 : p.s1;
+    const uint32_t *w = a == 0 ? p.w0 + call * p.w0_cs : p.w1 + call * p.w1_cs;
+    const float *sc = a == 0 ? p.s0 + call * p.s0_cs : p.s1 + call * p.s1_cs;
     float tot = 0.f;
     for (int grp = 0; grp < kg; grp++) {
       float part = 0.f;
@@ -296,34 +322,40 @@ __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
     }
     acc[a] = tot;
   }
+  const float *b0 = p.b0 ? p.b0 + call * p.b0_cs : nullptr;
+  const float *b1 = p.b1 ? p.b1 + call * p.b1_cs : nullptr;
   float v;
   if (MODE == MODE_UP) {
-    float b0 = p.b0 ? p.b0[(int64_t)e * p.N + n] : 0.f;
-    float b1 = p.b1 ? p.b1[(int64_t)e * p.N + n] : 0.f;
-    v = swiglu(acc[0] + b0, acc[1] + b1);
+    float bb0 = b0 ? b0[(int64_t)e * p.N + n] : 0.f;
+    float bb1 = b1 ? b1[(int64_t)e * p.N + n] : 0.f;
+    v = swiglu(acc[0] + bb0, acc[1] + bb1);
   } else {
-    v = acc[0] + (p.b0 ? p.b0[(int64_t)e * p.N + n] : 0.f);
+    v = acc[0] + (b0 ? b0[(int64_t)e * p.N + n] : 0.f);
   }
-  p.out[asg * p.N + n] = v;
+  p.out[call * p.out_cs + asg * p.N + n] = v;
 }
 
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s], slots in order; rows of
 // ids that are not experts contribute nothing. Reads, never scatters.
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y,
-                                                 const float *__restrict__ route,
-                                                 const float *__restrict__ residual, int T, int N,
-                                                 int E, int k, float *__restrict__ out) {
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, int64_t y_cs,
+                                                 const float *__restrict__ route, int64_t route_cs,
+                                                 const float *__restrict__ residual, int64_t res_cs,
+                                                 int T, int N, int E, int k,
+                                                 float *__restrict__ out, int64_t out_cs) {
+  const int call = blockIdx.z;
   const int t = blockIdx.x;
   const int n = blockIdx.y * 256 + threadIdx.x;
   if (n >= N) return;
-  float acc = residual ? residual[(int64_t)t * N + n] : 0.f;
+  y += call * y_cs;
+  route += call * route_cs;
+  float acc = residual ? residual[call * res_cs + (int64_t)t * N + n] : 0.f;
   for (int s = 0; s < k; s++) {
     const int64_t asg = (int64_t)t * k + s;
     if (route_expert(route, asg, k, E) < 0) continue;
     const float gate = route[(int64_t)t * 2 * k + k + s];
     acc = fmaf(gate, y[asg * N + n], acc);
   }
-  out[(int64_t)t * N + n] = acc;
+  out[call * out_cs + (int64_t)t * N + n] = acc;
 }
 
 __global__ void k_zero(float *__restrict__ p, size_t n) {
@@ -333,18 +365,17 @@ __global__ void k_zero(float *__restrict__ p, size_t n) {
 }
 
 template <int MODE>
-int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, const DispatchBufs &db,
-                hipStream_t s) {
+int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
   const bool mfma = ea.bits == 8 && (ea.g == ea.K || ea.g % 32 == 0);
   const int max_active = ea.E < ea.A ? ea.E : ea.A;
   if (mfma) {
-    dim3 grid((ea.N / 4 + 15) / 16, max_active), block(256);
+    dim3 grid((ea.N / 4 + 15) / 16, max_active, ea.calls), block(256);
     if (ea.a_dtype == MOE_F16)
       hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16>), grid, block, 0, s, p);
     else
       hipLaunchKernelGGL((k_expert_skinny<MODE, float>), grid, block, 0, s, p);
   } else {
-    dim3 grid(ea.A, (ea.N + 255) / 256), block(256);
+    dim3 grid(ea.A, (ea.N + 255) / 256, ea.calls), block(256);
     if (ea.a_dtype == MOE_F16)
       hipLaunchKernelGGL((k_expert_simple<MODE, _Float16>), grid, block, 0, s, p);
     else
@@ -358,51 +389,59 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, const DispatchBufs &
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   MOE_NONNULL(ea.a);
   MOE_NONNULL(ea.route);
-  MOE_NONNULL(ea.w0);
-  MOE_NONNULL(ea.w0->w);
-  MOE_NONNULL(ea.w0->scales);
+  MOE_NONNULL(ea.w0.w);
+  MOE_NONNULL(ea.w0.scales);
   MOE_NONNULL(ea.out);
   if (ea.mode == MODE_UP) {
-    MOE_NONNULL(ea.w1);
-    MOE_NONNULL(ea.w1->w);
-    MOE_NONNULL(ea.w1->scales);
+    MOE_NONNULL(ea.w1.w);
+    MOE_NONNULL(ea.w1.scales);
   }
   MOE_NONNULL(db.perm);
   MOE_NONNULL(db.offsets);
   MOE_NONNULL(db.active);
   MOE_NONNULL(db.meta);
+  if (db.E != ea.E || db.A != ea.A)
+    return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch workspace sized for another shape");
   ExpertKArgs p;
   p.a = ea.a;
+  p.a_cs = ea.a_cs;
   p.a_row_div = ea.a_row_div;
   p.route = ea.route;
+  p.route_cs = ea.route_cs;
   p.k = ea.k;
-  p.w0 = ea.w0->w;
-  p.s0 = ea.w0->scales;
-  p.b0 = ea.w0->bias;
-  p.w1 = ea.w1 ? ea.w1->w : nullptr;
-  p.s1 = ea.w1 ? ea.w1->scales : nullptr;
-  p.b1 = ea.w1 ? ea.w1->bias : nullptr;
+  p.w0 = ea.w0.w;
+  p.s0 = ea.w0.scales;
+  p.b0 = ea.w0.bias;
+  p.w1 = ea.w1.w;
+  p.s1 = ea.w1.scales;
+  p.b1 = ea.w1.bias;
+  p.w0_cs = ea.w0_cs;
+  p.s0_cs = ea.s0_cs;
+  p.b0_cs = ea.b0_cs;
+  p.w1_cs = ea.w1_cs;
+  p.s1_cs = ea.s1_cs;
+  p.b1_cs = ea.b1_cs;
   p.K = ea.K;
   p.N = ea.N;
   p.E = ea.E;
   p.bits = ea.bits;
   p.g = ea.g;
   p.out = ea.out;
-  p.perm = db.perm;
-  p.offsets = db.offsets;
-  p.active = db.active;
-  p.meta = db.meta;
-  if (ea.mode == MODE_UP) return launch_mode<MODE_UP>(ea, p, db, s);
-  return launch_mode<MODE_DOWN>(ea, p, db, s);
+  p.out_cs = ea.out_cs;
+  p.db = db;
+  if (ea.mode == MODE_UP) return launch_mode<MODE_UP>(ea, p, s);
+  return launch_mode<MODE_DOWN>(ea, p, s);
 }
 
-int launch_combine(const float *y, const float *route, const float *residual, int T, int N, int E,
-                   int k, float *out, hipStream_t s) {
+int launch_combine(const float *y, int64_t y_cs, const float *route, int64_t route_cs,
+                   const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
+                   int64_t out_cs, int calls, hipStream_t s) {
   MOE_NONNULL(y);
   MOE_NONNULL(route);
   MOE_NONNULL(out);
-  dim3 grid(T, (N + 255) / 256), block(256);
-  hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, route, residual, T, N, E, k, out);
+  dim3 grid(T, (N + 255) / 256, calls), block(256);
+  hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, route, route_cs, residual, res_cs, T,
+                     N, E, k, out, out_cs);
   return 0;
 }
 

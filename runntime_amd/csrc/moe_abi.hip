@@ -21,6 +21,66 @@ int moe_fail(int code, const std::string &msg) {
 extern "C" const char *moe_last_error(void) { return g_last_error.c_str(); }
 extern "C" int moe_version(void) { return MOE_VERSION; }
 
+// ------------------------------------------------------------------ timing
+
+const char *const PROF_NAMES[PROF_GROUPS] = {"topk", "router", "dispatch", "up",
+                                             "down", "combine", "", ""};
+
+static hipEvent_t prof_event(moe_ctx *c) {
+  if (!c->prof_free.empty()) {
+    hipEvent_t e = c->prof_free.back();
+    c->prof_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+ProfScope::ProfScope(moe_ctx *c, int g) : ctx(c), group(g) {
+  if (!ctx->prof_on) return;
+  b = prof_event(ctx);
+  if (b) (void)hipEventRecord(b, ctx->stream);
+}
+
+ProfScope::~ProfScope() {
+  if (!ctx->prof_on || !b) return;
+  hipEvent_t e = prof_event(ctx);
+  if (!e) return;
+  (void)hipEventRecord(e, ctx->stream);
+  ctx->prof_pending.push_back({group, b, e});
+}
+
+extern "C" int moe_prof_enable(moe_ctx *ctx, int on) {
+  if (!ctx) return moe_fail(MOE_NOT_INITIALIZED, "moe_prof_enable: context is NULL");
+  ctx->prof_on = on != 0;
+  return MOE_OK;
+}
+
+extern "C" int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *count_out) {
+  if (!ctx) return moe_fail(MOE_NOT_INITIALIZED, "moe_prof_read: context is NULL");
+  MOE_HIP_CHECK(hipSetDevice(ctx->device));
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  for (auto &r : ctx->prof_pending) {
+    float ms = 0.f;
+    MOE_HIP_CHECK(hipEventElapsedTime(&ms, r.begin, r.end));
+    ctx->prof_ms[r.group] += ms;
+    ctx->prof_count[r.group] += 1;
+    ctx->prof_free.push_back(r.begin);
+    ctx->prof_free.push_back(r.end);
+  }
+  ctx->prof_pending.clear();
+  for (int g = 0; g < PROF_GROUPS; g++) {
+    if (ms_out) ms_out[g] = ctx->prof_ms[g];
+    if (count_out) count_out[g] = ctx->prof_count[g];
+    if (reset) {
+      ctx->prof_ms[g] = 0;
+      ctx->prof_count[g] = 0;
+    }
+  }
+  return MOE_OK;
+}
+
 // ------------------------------------------------------------------ context
 
 extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
@@ -87,6 +147,11 @@ extern "C" int moe_ctx_destroy(moe_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
+  for (auto &r : ctx->prof_pending) {
+    (void)hipEventDestroy(r.begin);
+    (void)hipEventDestroy(r.end);
+  }
+  for (auto e : ctx->prof_free) (void)hipEventDestroy(e);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   ctx->disposed = true;
   delete ctx;
@@ -135,7 +200,7 @@ static int check_weight(const char *op, const moe_expert_weight *w, int K, int N
   return MOE_OK;
 }
 
-// ------------------------------------------------------------- dispatch ws
+// ------------------------------------------------------------- workspace
 
 struct LayerWs {
   DispatchBufs db;
@@ -145,24 +210,25 @@ struct LayerWs {
   float *y = nullptr;
 };
 
-// Workspace for a call over T tokens (A = T·k assignments). Sections that a
-// call does not need have size 0.
-static int plan_ws(moe_ctx *ctx, int T, int k, int E, size_t route_floats, size_t partial_floats,
-                   size_t act_floats, size_t y_floats, LayerWs &L) {
-  int A = T * k;
-  int nblk = (A + DISPATCH_TILE - 1) / DISPATCH_TILE;
+// Workspace for `calls` calls over T tokens each (A = T·k assignments per
+// call). Sections that a call does not need have size 0.
+static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_floats,
+                   size_t partial_floats, size_t act_floats, size_t y_floats, LayerWs &L) {
+  const int A = T * k;
+  const int nblk = (A + DISPATCH_TILE - 1) / DISPATCH_TILE;
+  const size_t C = (size_t)calls;
   WsPlan p;
-  size_t o_cnt = p.take(sizeof(int32_t) * (size_t)nblk * E);
-  size_t o_base = p.take(sizeof(int32_t) * (size_t)nblk * E);
-  size_t o_off = p.take(sizeof(int32_t) * (E + 1));
-  size_t o_toff = p.take(sizeof(int32_t) * (E + 1));
-  size_t o_act_list = p.take(sizeof(int32_t) * E);
-  size_t o_meta = p.take(sizeof(int32_t) * META_N);
-  size_t o_perm = p.take(sizeof(int32_t) * (size_t)A);
-  size_t o_route = p.take(sizeof(float) * route_floats);
-  size_t o_part = p.take(sizeof(float) * partial_floats);
-  size_t o_actv = p.take(sizeof(float) * act_floats);
-  size_t o_y = p.take(sizeof(float) * y_floats);
+  size_t o_cnt = p.take(sizeof(int32_t) * C * nblk * E);
+  size_t o_base = p.take(sizeof(int32_t) * C * nblk * E);
+  size_t o_off = p.take(sizeof(int32_t) * C * (E + 1));
+  size_t o_toff = p.take(sizeof(int32_t) * C * (E + 1));
+  size_t o_act_list = p.take(sizeof(int32_t) * C * E);
+  size_t o_meta = p.take(sizeof(int32_t) * C * META_N);
+  size_t o_perm = p.take(sizeof(int32_t) * C * A);
+  size_t o_route = p.take(sizeof(float) * C * route_floats);
+  size_t o_part = p.take(sizeof(float) * C * partial_floats);
+  size_t o_actv = p.take(sizeof(float) * C * act_floats);
+  size_t o_y = p.take(sizeof(float) * C * y_floats);
   int rc = moe_ws_ensure(ctx, p.off);
   if (rc) return rc;
   char *b = ctx->ws;
@@ -173,6 +239,9 @@ static int plan_ws(moe_ctx *ctx, int T, int k, int E, size_t route_floats, size_
   L.db.active = (int32_t *)(b + o_act_list);
   L.db.meta = (int32_t *)(b + o_meta);
   L.db.perm = (int32_t *)(b + o_perm);
+  L.db.E = E;
+  L.db.A = A;
+  L.db.nblk = nblk;
   L.route = route_floats ? (float *)(b + o_route) : nullptr;
   L.partial = partial_floats ? (float *)(b + o_part) : nullptr;
   L.act = act_floats ? (float *)(b + o_actv) : nullptr;
@@ -189,6 +258,10 @@ static int after_launch(const char *op) {
   return MOE_OK;
 }
 
+static int router_partial_floats(int T, int d, int E) {
+  return T * ((d + ROUTER_CHUNK - 1) / ROUTER_CHUNK) * E;
+}
+
 // ------------------------------------------------------------------- ops
 
 extern "C" int moe_topk(moe_ctx *ctx, const void *logits, moe_dtype dtype, int T, int E, int k,
@@ -200,7 +273,10 @@ extern "C" int moe_topk(moe_ctx *ctx, const void *logits, moe_dtype dtype, int T
   REQUIRE(E <= TOPK_MAX_E, "topk: more than " + S(TOPK_MAX_E) + " columns");
   REQUIRE(logits && route, "topk: NULL tensor");
   REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "topk: dtype must be f32 or f16");
-  if ((rc = launch_topk(logits, dtype, T, E, k, route, ctx->stream))) return rc;
+  {
+    ProfScope ps(ctx, PG_TOPK);
+    if ((rc = launch_topk(logits, dtype, T, E, k, route, ctx->stream))) return rc;
+  }
   return after_launch("topk");
 }
 
@@ -213,13 +289,13 @@ extern "C" int moe_router_topk(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
   REQUIRE(T >= 1 && d >= 1, "router_topk: T and d must be positive");
   REQUIRE(E <= ROUTER_MAX_E, "router_topk: more than " + S(ROUTER_MAX_E) + " experts");
   REQUIRE(x && w_router && route, "router_topk: NULL tensor");
-  int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-  WsPlan p;
-  p.take(sizeof(float) * (size_t)T * J * E);
-  if ((rc = moe_ws_ensure(ctx, p.off))) return rc;
-  if ((rc = launch_router_topk(x, x_dtype, w_router, b_router, T, d, E, k, (float *)ctx->ws, route,
-                               ctx->stream)))
-    return rc;
+  LayerWs L;
+  if ((rc = plan_ws(ctx, 1, T, k, E, 0, router_partial_floats(T, d, E), 0, 0, L))) return rc;
+  RouterArgs ra{x, x_dtype, 0, w_router, 0, b_router, 0, route, 0, L.partial, T, d, E, k, 1};
+  {
+    ProfScope ps(ctx, PG_ROUTER);
+    if ((rc = launch_router_topk(ra, nullptr, TILE_M, nullptr, ctx->stream))) return rc;
+  }
   return after_launch("router_topk");
 }
 
@@ -228,10 +304,13 @@ extern "C" int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int 
   int rc = check_ctx(ctx, "dispatch");
   if (rc) return rc;
   if ((rc = check_k("dispatch", k, E, false))) return rc;
-  REQUIRE(T >= 1 && E <= 1024, "dispatch: T ≥ 1 and E ≤ 1024 required");
+  REQUIRE(T >= 1 && E <= DISPATCH_MAX_E, "dispatch: T >= 1 and E <= 1024 required");
   LayerWs L;
-  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, 0, L))) return rc;
-  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
+  if ((rc = plan_ws(ctx, 1, T, k, E, 0, 0, 0, 0, L))) return rc;
+  {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, ctx->stream))) return rc;
+  }
   if (perm)
     MOE_HIP_CHECK(hipMemcpyAsync(perm, L.db.perm, sizeof(int32_t) * (size_t)T * k,
                                  hipMemcpyDeviceToDevice, ctx->stream));
@@ -252,13 +331,35 @@ extern "C" int moe_up(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
   REQUIRE(T >= 1, "moeUp: T must be at least 1");
   REQUIRE(x && route && act, "moeUp: NULL tensor");
   LayerWs L;
-  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, 0, L))) return rc;
-  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
+  if ((rc = plan_ws(ctx, 1, T, k, E, 0, 0, 0, 0, L))) return rc;
+  {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, ctx->stream))) return rc;
+  }
   // Rows of ids that are not experts stay zero (the reference leaves them
   // undefined).
   if ((rc = launch_zero(act, (size_t)T * k * N, ctx->stream))) return rc;
-  ExpertArgs ea{MODE_UP, x, x_dtype, k, route, k, glu, lin, K, N, E, bits, group_size, act, T * k};
-  if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
+  ExpertArgs ea{};
+  ea.mode = MODE_UP;
+  ea.a = x;
+  ea.a_dtype = x_dtype;
+  ea.a_row_div = k;
+  ea.route = route;
+  ea.k = k;
+  ea.w0 = *glu;
+  ea.w1 = *lin;
+  ea.K = K;
+  ea.N = N;
+  ea.E = E;
+  ea.bits = bits;
+  ea.g = group_size;
+  ea.out = act;
+  ea.A = T * k;
+  ea.calls = 1;
+  {
+    ProfScope ps(ctx, PG_UP);
+    if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
+  }
   return after_launch("moeUp");
 }
 
@@ -272,20 +373,48 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
   REQUIRE(T >= 1, "moeDown: T must be at least 1");
   REQUIRE(act && route && out, "moeDown: NULL tensor");
   LayerWs L;
-  if ((rc = plan_ws(ctx, T, k, E, 0, 0, 0, (size_t)T * k * N, L))) return rc;
-  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, ctx->stream))) return rc;
-  ExpertArgs ea{MODE_DOWN, act, MOE_F32, 1, route, k, down, nullptr, K, N, E, bits, group_size,
-                L.y, T * k};
-  if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
-  if ((rc = launch_combine(L.y, route, residual, T, N, E, k, out, ctx->stream))) return rc;
+  if ((rc = plan_ws(ctx, 1, T, k, E, 0, 0, 0, (size_t)T * k * N, L))) return rc;
+  {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, ctx->stream))) return rc;
+  }
+  ExpertArgs ea{};
+  ea.mode = MODE_DOWN;
+  ea.a = act;
+  ea.a_dtype = MOE_F32;
+  ea.a_row_div = 1;
+  ea.route = route;
+  ea.k = k;
+  ea.w0 = *down;
+  ea.K = K;
+  ea.N = N;
+  ea.E = E;
+  ea.bits = bits;
+  ea.g = group_size;
+  ea.out = L.y;
+  ea.A = T * k;
+  ea.calls = 1;
+  {
+    ProfScope ps(ctx, PG_DOWN);
+    if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_COMBINE);
+    if ((rc = launch_combine(L.y, 0, route, 0, residual, 0, T, N, E, k, out, 0, 1, ctx->stream)))
+      return rc;
+  }
   return after_launch("moeDown");
 }
 
-extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
-                         const float *b_router, const moe_expert_weight *glu,
-                         const moe_expert_weight *lin, const moe_expert_weight *down,
-                         const float *residual, int T, int d, int I, int E, int k, int bits,
-                         int group_size_up, int group_size_down, float *route_out, float *out) {
+static const moe_call_strides kZeroStrides = {};
+
+extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides *st,
+                                 const void *x, moe_dtype x_dtype, const float *w_router,
+                                 const float *b_router, const moe_expert_weight *glu,
+                                 const moe_expert_weight *lin, const moe_expert_weight *down,
+                                 const float *residual, int T, int d, int I, int E, int k,
+                                 int bits, int group_size_up, int group_size_down,
+                                 float *route_out, float *out) {
   int rc = check_ctx(ctx, "moe_layer");
   if (rc) return rc;
   if ((rc = check_k("moe_layer", k, E, true))) return rc;
@@ -293,33 +422,118 @@ extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const f
   if ((rc = check_weight("moe_layer", lin, d, I, E, bits, group_size_up))) return rc;
   if ((rc = check_weight("moe_layer", down, I, d, E, bits, group_size_down))) return rc;
   REQUIRE(T >= 1, "moe_layer: T must be at least 1");
+  REQUIRE(calls >= 1 && calls <= 65535, "moe_layer: calls must be in 1..65535, got " + S(calls));
   REQUIRE(E <= ROUTER_MAX_E, "moe_layer: more than " + S(ROUTER_MAX_E) + " experts");
   REQUIRE(x && w_router && out, "moe_layer: NULL tensor");
+  if (!st) st = &kZeroStrides;
+  if (calls > 1)
+    REQUIRE(st->x != 0 && st->out != 0 && (!route_out || st->route != 0),
+            "moe_layer: calls > 1 need distinct x, out and route_out (non-zero strides)");
   const int A = T * k;
-  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
   LayerWs L;
-  if ((rc = plan_ws(ctx, T, k, E, route_out ? 0 : (size_t)T * 2 * k, (size_t)T * J * E,
-                    (size_t)A * I, (size_t)A * d, L)))
+  if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
+                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)A * d, L)))
     return rc;
   float *route = route_out ? route_out : L.route;
+  const int64_t route_cs = route_out ? st->route : (int64_t)T * 2 * k;
   hipStream_t s = ctx->stream;
-  if ((rc = launch_router_topk(x, x_dtype, w_router, b_router, T, d, E, k, L.partial, route, s)))
-    return rc;
-  if ((rc = launch_dispatch(route, T, E, k, TILE_M, L.db, s))) return rc;
-  ExpertArgs up{MODE_UP, x, x_dtype, k, route, k, glu, lin, d, I, E, bits, group_size_up, L.act, A};
-  if ((rc = launch_expert(up, L.db, s))) return rc;
-  ExpertArgs dn{MODE_DOWN, L.act, MOE_F32, 1, route, k, down, nullptr, I, d, E, bits,
-                group_size_down, L.y, A};
-  if ((rc = launch_expert(dn, L.db, s))) return rc;
-  if ((rc = launch_combine(L.y, route, residual, T, d, E, k, out, s))) return rc;
+  bool dispatched = false;
+  {
+    ProfScope ps(ctx, PG_ROUTER);
+    RouterArgs ra{x, x_dtype, st->x, w_router, st->router_w, b_router, st->router_b, route,
+                  route_cs, L.partial, T, d, E, k, calls};
+    if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
+  }
+  if (!dispatched) {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, route_cs, T, E, k, calls, TILE_M, L.db, s))) return rc;
+  }
+  ExpertArgs up{};
+  up.mode = MODE_UP;
+  up.a = x;
+  up.a_dtype = x_dtype;
+  up.a_cs = st->x;
+  up.a_row_div = k;
+  up.route = route;
+  up.route_cs = route_cs;
+  up.k = k;
+  up.w0 = *glu;
+  up.w1 = *lin;
+  up.w0_cs = st->glu_w;
+  up.s0_cs = st->glu_scales;
+  up.b0_cs = st->glu_bias;
+  up.w1_cs = st->lin_w;
+  up.s1_cs = st->lin_scales;
+  up.b1_cs = st->lin_bias;
+  up.K = d;
+  up.N = I;
+  up.E = E;
+  up.bits = bits;
+  up.g = group_size_up;
+  up.out = L.act;
+  up.out_cs = (int64_t)A * I;
+  up.A = A;
+  up.calls = calls;
+  {
+    ProfScope ps(ctx, PG_UP);
+    if ((rc = launch_expert(up, L.db, s))) return rc;
+  }
+  ExpertArgs dn{};
+  dn.mode = MODE_DOWN;
+  dn.a = L.act;
+  dn.a_dtype = MOE_F32;
+  dn.a_cs = (int64_t)A * I;
+  dn.a_row_div = 1;
+  dn.route = route;
+  dn.route_cs = route_cs;
+  dn.k = k;
+  dn.w0 = *down;
+  dn.w0_cs = st->down_w;
+  dn.s0_cs = st->down_scales;
+  dn.b0_cs = st->down_bias;
+  dn.K = I;
+  dn.N = d;
+  dn.E = E;
+  dn.bits = bits;
+  dn.g = group_size_down;
+  dn.out = L.y;
+  dn.out_cs = (int64_t)A * d;
+  dn.A = A;
+  dn.calls = calls;
+  {
+    ProfScope ps(ctx, PG_DOWN);
+    if ((rc = launch_expert(dn, L.db, s))) return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_COMBINE);
+    if ((rc = launch_combine(L.y, (int64_t)A * d, route, route_cs, residual, st->residual, T, d,
+                             E, k, out, st->out, calls, s)))
+      return rc;
+  }
   return after_launch("moe_layer");
 }
 
+extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
+                         const float *b_router, const moe_expert_weight *glu,
+                         const moe_expert_weight *lin, const moe_expert_weight *down,
+                         const float *residual, int T, int d, int I, int E, int k, int bits,
+                         int group_size_up, int group_size_down, float *route_out, float *out) {
+  return moe_layer_batched(ctx, 1, nullptr, x, x_dtype, w_router, b_router, glu, lin, down,
+                           residual, T, d, I, E, k, bits, group_size_up, group_size_down,
+                           route_out, out);
+}
+
 extern "C" int moe_ctx_reserve(moe_ctx *ctx, int T, int d, int I, int E, int k) {
+  return moe_ctx_reserve_batched(ctx, 1, T, d, I, E, k);
+}
+
+extern "C" int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, int I, int E,
+                                       int k) {
   int rc = check_ctx(ctx, "moe_ctx_reserve");
   if (rc) return rc;
-  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  REQUIRE(calls >= 1 && T >= 1 && d >= 1 && I >= 1 && E >= 1 && k >= 1,
+          "moe_ctx_reserve: sizes must be positive");
   LayerWs L;
-  return plan_ws(ctx, T, k, E, (size_t)T * 2 * k, (size_t)T * J * E, (size_t)T * k * I,
-                 (size_t)T * k * (d > I ? d : I), L);
+  return plan_ws(ctx, calls, T, k, E, (size_t)T * 2 * k, router_partial_floats(T, d, E),
+                 (size_t)T * k * I, (size_t)T * k * (d > I ? d : I), L);
 }

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/runntime_moe.h"
 
@@ -24,6 +25,14 @@ int moe_fail(int code, const std::string &msg);
 
 // ----------------------------------------------------------------- context
 
+// Per-kernel-group timing (the reference's GpuPerfSink, src/core/gpu/perf.ts):
+// an event pair around every launch group while enabled, resolved on read.
+constexpr int PROF_GROUPS = 8;
+struct ProfRecord {
+  int group;
+  hipEvent_t begin, end;
+};
+
 struct moe_ctx {
   int device = 0;
   hipStream_t stream = nullptr;      // stream the calls enqueue on
@@ -31,6 +40,24 @@ struct moe_ctx {
   char *ws = nullptr;                // device workspace
   size_t ws_size = 0;
   bool disposed = false;
+  bool prof_on = false;
+  std::vector<ProfRecord> prof_pending;  // recorded, not yet resolved
+  std::vector<hipEvent_t> prof_free;     // reusable events
+  double prof_ms[PROF_GROUPS] = {};
+  int64_t prof_count[PROF_GROUPS] = {};
+};
+
+// Kernel groups the timing sink reports.
+enum ProfGroup { PG_TOPK = 0, PG_ROUTER = 1, PG_DISPATCH = 2, PG_UP = 3, PG_DOWN = 4, PG_COMBINE = 5 };
+extern const char *const PROF_NAMES[PROF_GROUPS];
+
+// Brackets the launches of one group with events when timing is on.
+struct ProfScope {
+  moe_ctx *ctx;
+  int group;
+  hipEvent_t b = nullptr;
+  ProfScope(moe_ctx *c, int g);
+  ~ProfScope();
 };
 
 // Bump allocator over the context workspace. Sizes are rounded to 256 B.
@@ -62,15 +89,25 @@ constexpr int DISPATCH_MAX_E = 1024;
 // Device-side bookkeeping written by the dispatch scan (int32 each).
 enum MetaSlot { META_VALID = 0, META_ACTIVE = 1, META_MAXCNT = 2, META_TILES = 3, META_N = 8 };
 
-// Dispatch workspace views (all device pointers).
+// Largest token count whose routing and dispatch one block does (fused).
+constexpr int SMALL_T = 16;
+
+// Dispatch workspace of a batch of calls. Each call owns a slice: the
+// per-call sizes below are the strides between them.
 struct DispatchBufs {
-  int32_t *blk_counts;  // [nblk, E]
-  int32_t *blk_base;    // [nblk, E]
-  int32_t *offsets;     // [E + 1]
-  int32_t *tile_off;    // [E + 1] cumulative M-tiles per expert
-  int32_t *active;      // [E] ids of experts with rows, ascending
-  int32_t *meta;        // [META_N]
-  int32_t *perm;        // [A] sorted position → assignment
+  int32_t *blk_counts;  // [nblk, E] per call
+  int32_t *blk_base;    // [nblk, E] per call
+  int32_t *offsets;     // [E + 1] per call
+  int32_t *tile_off;    // [E + 1] per call: cumulative M-tiles per expert
+  int32_t *active;      // [E] per call: ids of experts with rows, ascending
+  int32_t *meta;        // [META_N] per call
+  int32_t *perm;        // [A] per call: sorted position → assignment
+  int E, A, nblk;       // sizes that give the per-call strides
+  __host__ __device__ int64_t cnt_cs() const { return (int64_t)nblk * E; }
+  __host__ __device__ int64_t off_cs() const { return (int64_t)E + 1; }
+  __host__ __device__ int64_t act_cs() const { return E; }
+  __host__ __device__ int64_t meta_cs() const { return META_N; }
+  __host__ __device__ int64_t perm_cs() const { return A; }
 };
 
 // ---------------------------------------------------------- launchers
@@ -81,12 +118,32 @@ struct DispatchBufs {
     if (!(ptr)) return moe_fail(MOE_EXECUTION_FAILED, std::string(__func__) + ": " #ptr " is NULL"); \
   } while (0)
 
+// Every launcher takes `calls` independent calls of identical shape; call c
+// reads and writes each tensor at base + c·stride (elements; words for
+// quantW). A stride of 0 shares the tensor between calls.
+
 int launch_topk(const void *logits, moe_dtype dt, int T, int E, int k, float *route,
                 hipStream_t s);
-int launch_router_topk(const void *x, moe_dtype dt, const float *w, const float *b, int T, int d,
-                       int E, int k, float *partial, float *route, hipStream_t s);
-int launch_dispatch(const float *route, int T, int E, int k, int tile_m, const DispatchBufs &db,
-                    hipStream_t s);
+
+struct RouterArgs {
+  const void *x;
+  moe_dtype x_dtype;
+  int64_t x_cs;
+  const float *w;
+  int64_t w_cs;
+  const float *b;  // may be NULL
+  int64_t b_cs;
+  float *route;
+  int64_t route_cs;
+  float *partial;  // workspace, T·J·E floats per call
+  int T, d, E, k, calls;
+};
+// Router + top-k. With T <= SMALL_T and `db` given, the dispatch of each call
+// is built in the same kernel and `dispatched` is set.
+int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m, bool *dispatched,
+                       hipStream_t s);
+int launch_dispatch(const float *route, int64_t route_cs, int T, int E, int k, int calls,
+                    int tile_m, const DispatchBufs &db, hipStream_t s);
 
 enum ExpertMode { MODE_UP = 0, MODE_DOWN = 1 };
 
@@ -94,19 +151,26 @@ struct ExpertArgs {
   int mode;                 // ExpertMode
   const void *a;            // x [T, K] (up) or act [T·k, K] (down)
   moe_dtype a_dtype;
+  int64_t a_cs;
   int a_row_div;            // source row = assignment / a_row_div (k for up, 1 for down)
   const float *route;       // [T, 2k]
+  int64_t route_cs;
   int k;
-  const moe_expert_weight *w0;  // glu (up) or down
-  const moe_expert_weight *w1;  // lin (up) or null
+  moe_expert_weight w0;     // glu (up) or down
+  moe_expert_weight w1;     // lin (up); unused for down
+  int64_t w0_cs, s0_cs, b0_cs, w1_cs, s1_cs, b1_cs;
   int K, N, E, bits, g;
   float *out;               // act [T·k, N] (up) or y [T·k, N] (down), row = assignment
+  int64_t out_cs;
   int A;                    // T·k
+  int calls;
 };
 
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 // Fills n floats with 0 (a kernel, not hipMemsetAsync, so a captured graph
 // replays it correctly).
 int launch_zero(float *p, size_t n, hipStream_t s);
-int launch_combine(const float *y, const float *route, const float *residual, int T, int N, int E,
-                   int k, float *out, hipStream_t s);
+// out[t] = residual[t] + Σ_s gate_s · y[t·k + s] per call.
+int launch_combine(const float *y, int64_t y_cs, const float *route, int64_t route_cs,
+                   const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
+                   int64_t out_cs, int calls, hipStream_t s);

@@ -17,7 +17,7 @@
 // wavefront: a logit is a candidate only if it is strictly above the
 // reference's −3.4e38 start value (so NaN never enters), and a slot no
 // candidate fills keeps (−3.4e38, id 0), as the reference's does.
-#include "moe_internal.h"
+#include "dispatch_dev.h"
 
 namespace {
 
@@ -44,8 +44,8 @@ __device__ __forceinline__ void wave_argmax(float &v, int &e) {
 // Then w_i = exp(v_i − v_0) / Σ_j exp(v_j − v_0), the sum taken left to right
 // (topkSelect.ts:142-156); lane i < k writes slot i.
 template <int NI>
-__device__ __forceinline__ void wave_topk_route(const float (&vals)[NI], int E, int k, int lane,
-                                                float *row) {
+__device__ __forceinline__ int wave_topk_route(const float (&vals)[NI], int E, int k, int lane,
+                                               float *row) {
   uint64_t taken = 0;
   float my_v = NEG_START;
   int my_id = 0;
@@ -85,6 +85,7 @@ __device__ __forceinline__ void wave_topk_route(const float (&vals)[NI], int E, 
     row[lane] = (float)my_id;
     row[k + lane] = ex / z;
   }
+  return my_id;
 }
 
 // ------------------------------------------------------- standalone topk
@@ -106,24 +107,28 @@ __global__ __launch_bounds__(256) void k_topk(const T *__restrict__ logits, int 
 
 // --------------------------------------------------------- fused router
 
-// Per (token tile, d chunk, expert tile): c_j for every (token, expert). The
-// x tile [16, 64] and the W chunk [64, 128] sit in LDS.
+// Per (token tile, d chunk, expert tile, call): c_j for every (token,
+// expert). The x tile [16, 64] and the W chunk [64, 128] sit in LDS.
 constexpr int RT_TOKENS = 16;
 constexpr int RT_EXPERTS = 128;
 
 template <typename T>
-__global__ __launch_bounds__(256) void k_router_chunks(const T *__restrict__ x,
-                                                       const float *__restrict__ w, int Tn, int d,
-                                                       int E, float *__restrict__ partial) {
+__global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   __shared__ float xs[RT_TOKENS * ROUTER_CHUNK];
   __shared__ float ws[ROUTER_CHUNK * RT_EXPERTS];
-  int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-  int t0 = blockIdx.x * RT_TOKENS;
-  int j = blockIdx.y;
-  int e0 = blockIdx.z * RT_EXPERTS;
-  int et = min(RT_EXPERTS, E - e0);
-  int k0 = j * ROUTER_CHUNK;
-  int len = min(ROUTER_CHUNK, d - k0);
+  const int Tn = ra.T, d = ra.d, E = ra.E;
+  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const int etiles = (E + RT_EXPERTS - 1) / RT_EXPERTS;
+  const int call = blockIdx.z / etiles;
+  const T *x = (const T *)ra.x + call * ra.x_cs;
+  const float *w = ra.w + call * ra.w_cs;
+  float *partial = ra.partial + call * ((int64_t)Tn * J * E);
+  const int t0 = blockIdx.x * RT_TOKENS;
+  const int j = blockIdx.y;
+  const int e0 = (blockIdx.z % etiles) * RT_EXPERTS;
+  const int et = min(RT_EXPERTS, E - e0);
+  const int k0 = j * ROUTER_CHUNK;
+  const int len = min(ROUTER_CHUNK, d - k0);
   for (int i = threadIdx.x; i < RT_TOKENS * ROUTER_CHUNK; i += blockDim.x) {
     int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
     int t = t0 + tt;
@@ -146,29 +151,85 @@ __global__ __launch_bounds__(256) void k_router_chunks(const T *__restrict__ x,
   }
 }
 
-// Folds the chunk partials in order, adds the bias and runs the top-k.
+// S = ((c_0 + c_1) + c_2) + … + b for the wavefront's experts: the J loads
+// are issued 8 at a time, the adds stay in chunk order.
 template <int NI>
-__global__ __launch_bounds__(256) void k_router_fold_topk(const float *__restrict__ partial,
-                                                          const float *__restrict__ b, int Tn,
-                                                          int J, int E, int k,
-                                                          float *__restrict__ route) {
-  int lane = threadIdx.x & (WAVE - 1);
-  int t = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
-  if (t >= Tn) return;
-  float vals[NI];
+__device__ __forceinline__ void fold_logits(const float *partial, const float *b, int t, int J,
+                                            int E, int lane, float (&vals)[NI]) {
 #pragma unroll
   for (int i = 0; i < NI; i++) {
-    int e = lane + WAVE * i;
+    const int e = lane + moe_dev::WAVE * i;
     float s = -INFINITY;
     if (e < E) {
       const float *p = partial + (int64_t)t * J * E + e;
       s = p[0];
-      for (int jj = 1; jj < J; jj++) s = s + p[(int64_t)jj * E];
+      int jj = 1;
+      for (; jj + 8 <= J; jj += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p[(int64_t)(jj + u) * E];
+#pragma unroll
+        for (int u = 0; u < 8; u++) s = s + v[u];
+      }
+      for (; jj < J; jj++) s = s + p[(int64_t)jj * E];
       if (b) s = s + b[e];
     }
     vals[i] = s;
   }
-  wave_topk_route<NI>(vals, E, k, lane, route + (int64_t)t * 2 * k);
+}
+
+// One wavefront per token: fold, top-k, route row.
+template <int NI>
+__global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
+  const int lane = threadIdx.x & (moe_dev::WAVE - 1);
+  const int t = blockIdx.x * (blockDim.x / moe_dev::WAVE) + threadIdx.x / moe_dev::WAVE;
+  if (t >= ra.T) return;
+  const int call = blockIdx.y;
+  const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const float *partial = ra.partial + call * ((int64_t)ra.T * J * ra.E);
+  const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
+  float vals[NI];
+  fold_logits<NI>(partial, b, t, J, ra.E, lane, vals);
+  wave_topk_route<NI>(vals, ra.E, ra.k, lane, ra.route + call * ra.route_cs + (int64_t)t * 2 * ra.k);
+}
+
+// Small calls (T <= 16): one block of 16 wavefronts per call does the fold
+// and top-k of every token, then the call's dispatch (dispatch_dev.h) from
+// the ids it just chose — no second pass over the route.
+template <int NI>
+__global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs ra, DispatchBufs db,
+                                                                    int tile_m) {
+  __shared__ int32_t sid[SMALL_T * MAX_K];
+  __shared__ int32_t hist[DISPATCH_MAX_E];
+  __shared__ int32_t cursor[DISPATCH_MAX_E + 1];
+  __shared__ int32_t wc[4 * DISPATCH_MAX_E];
+  const int lane = threadIdx.x & (moe_dev::WAVE - 1);
+  const int t = threadIdx.x / moe_dev::WAVE;
+  const int call = blockIdx.x;
+  const int E = ra.E, k = ra.k, A = ra.T * ra.k;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  if (t < ra.T) {
+    const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+    const float *partial = ra.partial + call * ((int64_t)ra.T * J * E);
+    const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
+    float vals[NI];
+    fold_logits<NI>(partial, b, t, J, E, lane, vals);
+    int id = wave_topk_route<NI>(vals, E, k, lane,
+                                 ra.route + call * ra.route_cs + (int64_t)t * 2 * k);
+    if (lane < k) sid[t * k + lane] = id;
+  }
+  __syncthreads();
+  const int a = threadIdx.x;
+  const int e = (a < A) ? sid[a] : -1;
+  if (e >= 0) atomicAdd(&hist[e], 1);
+  __syncthreads();
+  if (threadIdx.x < moe_dev::WAVE)
+    moe_dev::wave_scan_experts(hist, E, tile_m, lane, db.offsets + call * db.off_cs(),
+                               db.tile_off + call * db.off_cs(), db.active + call * db.act_cs(),
+                               db.meta + call * db.meta_cs(), cursor);
+  __syncthreads();
+  int32_t *perm = db.perm + call * db.perm_cs();
+  moe_dev::block_place(e, a, E, cursor, wc, perm);
 }
 
 template <typename T>
@@ -185,21 +246,6 @@ int topk_launch(const T *logits, int Tn, int E, int k, float *route, hipStream_t
   return moe_fail(MOE_INVALID_ARGUMENT, "topk: more than 4096 experts");
 }
 
-int fold_launch(const float *partial, const float *b, int Tn, int J, int E, int k, float *route,
-                hipStream_t s) {
-  dim3 grid((Tn + 3) / 4), block(256);
-  int ni = (E + WAVE - 1) / WAVE;
-#define FOLD_NI(N)                                                                          \
-  if (ni <= N) {                                                                            \
-    hipLaunchKernelGGL((k_router_fold_topk<N>), grid, block, 0, s, partial, b, Tn, J, E, k, \
-                       route);                                                              \
-    return 0;                                                                               \
-  }
-  FOLD_NI(1) FOLD_NI(2) FOLD_NI(4) FOLD_NI(8)
-#undef FOLD_NI
-  return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
-}
-
 }  // namespace
 
 int launch_topk(const void *logits, moe_dtype dt, int T, int E, int k, float *route,
@@ -210,19 +256,44 @@ int launch_topk(const void *logits, moe_dtype dt, int T, int E, int k, float *ro
   return topk_launch((const float *)logits, T, E, k, route, s);
 }
 
-int launch_router_topk(const void *x, moe_dtype dt, const float *w, const float *b, int T, int d,
-                       int E, int k, float *partial, float *route, hipStream_t s) {
-  MOE_NONNULL(x);
-  MOE_NONNULL(w);
-  MOE_NONNULL(partial);
-  MOE_NONNULL(route);
-  int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-  dim3 grid((T + RT_TOKENS - 1) / RT_TOKENS, J, (E + RT_EXPERTS - 1) / RT_EXPERTS), block(256);
-  if (dt == MOE_F16)
-    hipLaunchKernelGGL(k_router_chunks<_Float16>, grid, block, 0, s, (const _Float16 *)x, w, T,
-                       d, E, partial);
+int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m, bool *dispatched,
+                       hipStream_t s) {
+  MOE_NONNULL(ra.x);
+  MOE_NONNULL(ra.w);
+  MOE_NONNULL(ra.partial);
+  MOE_NONNULL(ra.route);
+  if (ra.E > ROUTER_MAX_E) return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
+  const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
+  dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
+  if (ra.x_dtype == MOE_F16)
+    hipLaunchKernelGGL(k_router_chunks<_Float16>, grid, block, 0, s, ra);
   else
-    hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, (const float *)x, w, T, d, E,
-                       partial);
-  return fold_launch(partial, b, T, J, E, k, route, s);
+    hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, ra);
+  const int ni = (ra.E + WAVE - 1) / WAVE;
+  const bool fuse = db && ra.T <= SMALL_T;
+  if (dispatched) *dispatched = fuse;
+  if (fuse) {
+    MOE_NONNULL(db->offsets);
+    MOE_NONNULL(db->perm);
+    if (db->E != ra.E || db->A != ra.T * ra.k)
+      return moe_fail(MOE_EXECUTION_FAILED, "router: dispatch workspace sized for another shape");
+#define FUSED_NI(N)                                                                        \
+  if (ni <= N) {                                                                           \
+    hipLaunchKernelGGL((k_router_fold_topk_dispatch<N>), dim3(ra.calls), dim3(1024), 0, s, ra, \
+                       *db, tile_m);                                                       \
+    return 0;                                                                              \
+  }
+    FUSED_NI(1) FUSED_NI(2) FUSED_NI(4) FUSED_NI(8)
+#undef FUSED_NI
+  }
+  dim3 g2((ra.T + 3) / 4, ra.calls);
+#define FOLD_NI(N)                                                                      \
+  if (ni <= N) {                                                                        \
+    hipLaunchKernelGGL((k_router_fold_topk<N>), g2, dim3(256), 0, s, ra);               \
+    return 0;                                                                           \
+  }
+  FOLD_NI(1) FOLD_NI(2) FOLD_NI(4) FOLD_NI(8)
+#undef FOLD_NI
+  return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
 }

@@ -126,3 +126,37 @@ def make_inputs(cfg: MoeConfig, seed: int = 0, device="cuda", keep_q: bool = Fal
     if keep_q:
         inp.q = {"glu": qg, "lin": ql, "down": qd}
     return inp
+
+
+@dataclass
+class WeightCopies:
+    """C independent copies of one layer's weights, stacked on a leading
+    call dim for moe_layer_batched."""
+    cfg: MoeConfig
+    router_w: torch.Tensor  # [C, d, E]
+    router_b: torch.Tensor  # [C, E]
+    glu: QuantExpertWeight  # words [C, n], scales [C, E, N], bias [C, E, N]
+    lin: QuantExpertWeight
+    down: QuantExpertWeight
+
+
+def make_weight_copies(cfg: MoeConfig, copies: int, seed: int = 0,
+                       device="cuda") -> WeightCopies:
+    """`copies` seeded weight sets drawn with a generator on `device` (the
+    bench's multi-GB sets are drawn on the GPU; same distributions as
+    make_inputs)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    C, E, d, I = copies, cfg.E, cfg.d, cfg.I
+
+    def ew(K, N):
+        q = torch.randint(-127, 128, (C * E, K, N), generator=g, dtype=torch.int8, device=device)
+        words = pack_expert_weights_torch(q).view(C, -1)
+        del q
+        sc = torch.rand((C, E, N), generator=g, dtype=torch.float32, device=device) * 1.5e-3 + 0.5e-3
+        return QuantExpertWeight(QuantW(words, (E * K, N)), sc,
+                                 torch.zeros((C, E, N), dtype=torch.float32, device=device))
+
+    rw = torch.randn((C, d, E), generator=g, dtype=torch.float32, device=device) * 0.02
+    rb = torch.zeros((C, E), dtype=torch.float32, device=device)
+    return WeightCopies(cfg, rw, rb, ew(d, I), ew(d, I), ew(I, d))

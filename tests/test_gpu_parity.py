@@ -296,3 +296,84 @@ def test_moe_layer_matches_ops():
     act = rt.moeUp(inp.x, r2, inp.glu, inp.lin, {"bits": 8, "groupSize": cfg.d})
     o2 = rt.moeDown(act, r2, inp.down, inp.residual, {"bits": 8, "groupSize": cfg.I})
     assert_close(host(out), host(o2), atol=1e-5, rtol=1e-5, what="layer vs ops")
+
+
+# --------------------------------------------------------- batched calls
+
+
+def _slice_weight(w, c):
+    return QuantExpertWeight(QuantW(w.w.words[c], w.w.dims), w.scales[c], w.bias[c])
+
+
+@pytest.mark.parametrize("T,cfg_id", [(1, 2), (5, 1), (40, 1)])
+def test_moe_layer_batched_equals_single_calls(T, cfg_id):
+    """Each call of a batch is the same computation as a standalone
+    moe_layer call on that call's slices (bit for bit), and the first call
+    matches the oracle."""
+    from runntime_amd.synth import make_weight_copies
+    cfg = CONFIGS[cfg_id]
+    C = 3
+    say(f"moe_layer_batched T={T} calls={C} {cfg.name}")
+    wc = make_weight_copies(cfg, C, seed=5, device="cpu")
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((C, T, cfg.d), generator=g)
+    res = torch.randn((C, T, cfg.d), generator=g)
+    wc.router_b.copy_(torch.randn((C, cfg.E), generator=g) * 0.1)
+    for w in (wc.glu, wc.lin, wc.down):
+        w.bias.copy_(torch.randn(w.bias.shape, generator=g) * 0.1)
+    dev = lambda t: t.to(DEV)
+    dw = lambda w: QuantExpertWeight(QuantW(dev(w.w.words), w.w.dims), dev(w.scales), dev(w.bias))
+    out, route = rt.moe_layer_batched(dev(x), dev(wc.router_w), dev(wc.router_b), dw(wc.glu),
+                                      dw(wc.lin), dw(wc.down), dev(res), cfg.k)
+    out, route = host(out), host(route)
+    for c in range(C):
+        o1, r1 = rt.moe_layer(dev(x[c]), dev(wc.router_w[c]), dev(wc.router_b[c]),
+                              dw(_slice_weight(wc.glu, c)), dw(_slice_weight(wc.lin, c)),
+                              dw(_slice_weight(wc.down, c)), dev(res[c]), cfg.k, return_route=True)
+        assert np.array_equal(host(r1), route[c])
+        assert np.array_equal(host(o1), out[c])
+    # call 0 against the oracle
+    xs = x[0].numpy()
+    want_route = ref.topk(ref.router_logits(xs, wc.router_w[0].numpy(), wc.router_b[0].numpy()),
+                          cfg.k)
+    assert np.array_equal(route[0][:, :cfg.k], want_route[:, :cfg.k])
+    wt = lambda w: (w.w.words[0].numpy().view(np.uint32), w.scales[0].numpy(), w.bias[0].numpy())
+    act = ref.moe_up(xs, want_route, wt(wc.glu), wt(wc.lin), 8, cfg.d, cfg.E)
+    want = ref.moe_down(act, want_route, wt(wc.down), res[0].numpy(), 8, cfg.I, cfg.E)
+    assert_close(out[0], want, what="batched call 0")
+
+
+def test_graph_replay_matches_eager():
+    """A captured moe_layer_batched replays correctly several times, with
+    eager work and synchronisation between the replays."""
+    from runntime_amd import perf
+    from runntime_amd.synth import make_weight_copies
+    cfg = CONFIGS[2]
+    C = 4
+    say("graph replay")
+    wc = make_weight_copies(cfg, C, seed=8, device=DEV)
+    x = torch.randn((C, 1, cfg.d), device=DEV)
+    res = torch.zeros((C, 1, cfg.d), device=DEV)
+    out = torch.empty((C, 1, cfg.d), device=DEV)
+    route = torch.empty((C, 1, 2 * cfg.k), device=DEV)
+    run = lambda: rt.moe_layer_batched(x, wc.router_w, wc.router_b, wc.glu, wc.lin, wc.down, res,
+                                       cfg.k, out=out, route=route)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        perf.reserve_batched(C, 1, cfg.d, cfg.I, cfg.E, cfg.k)
+        run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            run()
+        for i in range(4):
+            x.copy_(torch.randn((C, 1, cfg.d), device=DEV))
+            run()  # eager reference for these inputs
+            torch.cuda.synchronize()
+            want_out, want_route = out.clone(), route.clone()
+            out.zero_()
+            route.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(route, want_route), f"replay {i}: route"
+            assert torch.equal(out, want_out), f"replay {i}: out"
