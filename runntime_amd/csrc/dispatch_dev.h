@@ -24,7 +24,8 @@ __device__ __forceinline__ int route_expert(const float *route, int64_t a, int k
 }
 
 // One wavefront turns per-expert counts (LDS) into the call's offsets,
-// M-tile offsets, active list and meta. lds_off receives a copy of offsets.
+// M-tile offsets, active-expert descriptors {e, first row, rows, first
+// M-tile} and meta. lds_off receives a copy of offsets.
 // Lane l scans a contiguous chunk of experts; chunk totals are combined with
 // a shuffle prefix sum.
 __device__ __forceinline__ void wave_scan_experts(const int32_t *hist, int E, int tile_m, int lane,
@@ -62,13 +63,24 @@ __device__ __forceinline__ void wave_scan_experts(const int32_t *hist, int E, in
     offsets[e] = bc;
     lds_off[e] = bc;
     tile_off[e] = bt;
-    if (h > 0) active[ba++] = e;
+    if (h > 0) {
+      active[4 * ba + 0] = e;
+      active[4 * ba + 1] = bc;
+      active[4 * ba + 2] = h;
+      active[4 * ba + 3] = bt;
+      ba++;
+    }
     bc += h;
     bt += (h + tile_m - 1) / tile_m;
   }
   const int total = __shfl(ic, WAVE - 1), ttot = __shfl(it, WAVE - 1),
             atot = __shfl(ia, WAVE - 1);
-  for (int i = atot + lane; i < E; i += WAVE) active[i] = -1;
+  for (int i = atot + lane; i < E; i += WAVE) {
+    active[4 * i + 0] = -1;
+    active[4 * i + 1] = 0;
+    active[4 * i + 2] = 0;
+    active[4 * i + 3] = 0;
+  }
   if (lane == 0) {
     offsets[E] = total;
     lds_off[E] = total;

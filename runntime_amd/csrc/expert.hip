@@ -50,6 +50,7 @@ struct ExpertKArgs {
   int K, N, E, bits, g;
   float *out;
   int64_t out_cs;
+  int rc;  // rows staged per chunk (skinny kernel)
   DispatchBufs db;
 };
 
@@ -79,202 +80,252 @@ __device__ __forceinline__ half8 cvt_i8x8(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-// A fragment: 8 consecutive k of one row, as f16 hi (+ lo for f32 input).
+// A rows staged in LDS as f16: row r, k at rows[r·kp + k] (kp = K rounded
+// up to whole 32-wide K steps — the fragments of the last step read that far,
+// and the staging writes zeros there — plus 8 halves of padding that shifts
+// each row by 4 banks), and
+// for f32 input a second plane with the low parts: v = hi + lo to ~2^-22.
 template <typename AT>
-struct AFrag;
+struct AStage {
+  static constexpr bool SPLIT = sizeof(AT) == 4;
+  static constexpr int PLANES = SPLIT ? 2 : 1;
+};
 
-template <>
-struct AFrag<_Float16> {
-  static constexpr bool SPLIT = false;
-  __device__ __forceinline__ static void load(const void *base, int64_t row, int K, int k0,
-                                              bool valid, half8 &hi, half8 &lo) {
-    const _Float16 *p = (const _Float16 *)base + row * K + k0;
-    if (valid && k0 + 8 <= K && (K & 7) == 0) {
-      hi = *(const half8 *)p;
-    } else {
+__host__ __device__ __forceinline__ int a_stage_kp(int K) { return ((K + 31) & ~31) + 8; }
+
+// Rows per chunk that keep the staged A within 64 KB of LDS.
+__host__ __device__ __forceinline__ int a_stage_rows(int K, bool split) {
+  const int bytes_per_row = a_stage_kp(K) * 2 * (split ? 2 : 1);
+  int r = 16;
+  while (r > 1 && r * bytes_per_row > 65536) r >>= 1;
+  return r;
+}
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+// Lane group kq of a 32-wide K step holds k ∈ {4kq..4kq+3} ∪ {16+4kq..}: the
+// same k as the lane's B tiles (8·step + kq and 8·step + 4 + kq).
+__device__ __forceinline__ half8 a_frag(const _Float16 *plane, int kp, int row, int step, int kq) {
+  const _Float16 *p = plane + row * kp + step * 32 + 4 * kq;
+  half4 lo = *(const half4 *)p;
+  half4 hi = *(const half4 *)(p + 16);
+  half8 r;
 #pragma unroll
-      for (int j = 0; j < 8; j++) hi[j] = (valid && k0 + j < K) ? p[j] : (_Float16)0.0f;
-    }
-    (void)lo;
+  for (int j = 0; j < 4; j++) {
+    r[j] = lo[j];
+    r[4 + j] = hi[j];
   }
+  return r;
+}
+
+// Weight tiles of one K step of one wavefront.
+struct WStep {
+  uint4 t0, t1;
 };
 
-template <>
-struct AFrag<float> {
-  static constexpr bool SPLIT = true;
-  __device__ __forceinline__ static void load(const void *base, int64_t row, int K, int k0,
-                                              bool valid, half8 &hi, half8 &lo) {
-    const float *p = (const float *)base + row * K + k0;
-    float v[8];
-    if (valid && k0 + 8 <= K) {
-      floatx4 a = *(const floatx4 *)p;
-      floatx4 b = *(const floatx4 *)(p + 4);
-      v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
-      v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; j++) v[j] = (valid && k0 + j < K) ? p[j] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      _Float16 h = (_Float16)v[j];
-      hi[j] = h;
-      lo[j] = (_Float16)(v[j] - (float)h);
-    }
-  }
-};
-
-template <int NARR>
-struct WTiles {
-  uint4 t0[NARR], t1[NARR];
-};
-
-template <int MODE, typename AT>
+// k_expert_skinny: one block = one active expert × CGB groups of 64 output
+// columns (16 quantW units each). The expert's rows are taken RC at a time
+// (RC ≤ 16 keeps them in LDS); for each chunk the block stages the rows' A in
+// LDS once, then each wavefront streams one weight array for one column
+// group over the whole of K (up: {glu, lin} × 2 groups; down: 4 groups)
+// through a 3-stage register pipeline: the weight loads of steps s+1 and s+2
+// are in flight while step s converts and multiplies. A comes from LDS, so
+// its reads never wait behind the weight stream; scales and biases are
+// fetched before the stream starts. Up's glu and lin wavefronts meet in LDS
+// for the SwiGLU epilogue.
+// GROUPED: scales change along K (groupSize < K), so partial sums are
+// scaled per group; otherwise one scale per column is applied at the end.
+template <int MODE, typename AT, bool GROUPED>
 __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
   constexpr int NARR = (MODE == MODE_UP) ? 2 : 1;
-  __shared__ floatx4 red[4][NARR * 4][WAVE];
+  constexpr int CGB = 4 / NARR;  // column groups per block
+  constexpr bool SPLIT = AStage<AT>::SPLIT;
+  // LDS: the staged A rows during the K loop, then (same bytes) the lin
+  // wavefronts' sums [CGB][4][64] floatx4 for the up epilogue.
+  extern __shared__ __align__(16) unsigned char smem[];
+  floatx4 *red = (floatx4 *)smem;
+  _Float16 *ahi = (_Float16 *)smem;
 
   const int call = blockIdx.z;
-  const int32_t *meta = p.db.meta + call * p.db.meta_cs();
-  const int slot = blockIdx.y;
-  if (slot >= meta[META_ACTIVE]) return;
-  const int e = p.db.active[call * p.db.act_cs() + slot];
-  const int32_t *offsets = p.db.offsets + call * p.db.off_cs();
+  const int4 desc = ((const int4 *)(p.db.active + call * p.db.act_cs()))[blockIdx.y];
+  const int e = desc.x;
+  if (e < 0) return;
+  const int p0 = desc.y, cnt = desc.z;
   const int32_t *perm = p.db.perm + call * p.db.perm_cs();
-  const int p0 = offsets[e];
-  const int cnt = offsets[e + 1] - p0;
-  const void *abase = (const char *)p.a + call * p.a_cs * (int64_t)sizeof(AT);
+  const AT *abase = (const AT *)p.a + call * p.a_cs;
   float *out = p.out + call * p.out_cs;
-  const float *s0 = p.s0 + call * p.s0_cs;
-  const float *s1 = (NARR == 2) ? p.s1 + call * p.s1_cs : nullptr;
-  const float *b0 = p.b0 ? p.b0 + call * p.b0_cs : nullptr;
-  const float *b1 = (NARR == 2 && p.b1) ? p.b1 + call * p.b1_cs : nullptr;
 
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
+  const int arr = wave % NARR;  // weight array of this wavefront
+  const int cg = wave / NARR;   // column group of this wavefront
   const int N4 = p.N / 4, K4 = p.K / 4;
-  const int u = blockIdx.x * 16 + (lane & 15);
+  const int u = (blockIdx.x * CGB + cg) * 16 + (lane & 15);
   const bool uok = u < N4;
   const int kq = lane >> 4;
+  const int m = lane & 15;
   const int steps = (p.K + 31) / 32;
-  const int per = (steps + 3) / 4;
-  const int sb = wave * per;
-  const int se = min(steps, sb + per);
   const int kg = p.K / p.g;
+  const int kp = a_stage_kp(p.K);
+  const int RC = p.rc;
+  _Float16 *alo = ahi + RC * kp;
 
-  const uint4 *wt[2];
-  wt[0] = (const uint4 *)(p.w0 + call * p.w0_cs) + ((int64_t)e * N4 + (uok ? u : 0)) * K4;
-  wt[1] = (NARR == 2) ? (const uint4 *)(p.w1 + call * p.w1_cs) + ((int64_t)e * N4 + (uok ? u : 0)) * K4
-                      : nullptr;
+  const uint32_t *wbase = arr == 0 ? p.w0 + call * p.w0_cs : p.w1 + call * p.w1_cs;
+  const float *sc = arr == 0 ? p.s0 + call * p.s0_cs : p.s1 + call * p.s1_cs;
+  const float *bp = arr == 0 ? (p.b0 ? p.b0 + call * p.b0_cs : nullptr)
+                             : (p.b1 ? p.b1 + call * p.b1_cs : nullptr);
+  const uint4 *wt = (const uint4 *)wbase + ((int64_t)e * N4 + (uok ? u : 0)) * K4;
+  // This wavefront's 4 columns: scales (one group) and biases, fetched early.
+  const floatx4 s_one = (!GROUPED && uok) ? *(const floatx4 *)(sc + (int64_t)e * p.N + 4 * u)
+                                           : floatx4{0.f, 0.f, 0.f, 0.f};
+  const floatx4 bias4 = (bp && uok) ? *(const floatx4 *)(bp + (int64_t)e * p.N + 4 * u)
+                                    : floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto load_w = [&](int step, WTiles<NARR> &w) {
-    const int k4 = step * 8 + kq * 2;
-#pragma unroll
-    for (int a = 0; a < NARR; a++) {
-      w.t0[a] = (uok && k4 < K4) ? wt[a][k4] : uint4{0, 0, 0, 0};
-      w.t1[a] = (uok && k4 + 1 < K4) ? wt[a][k4 + 1] : uint4{0, 0, 0, 0};
-    }
+  // Tiles 8·step + kq and 8·step + 4 + kq: the 4 lanes of a unit read 64
+  // contiguous bytes per load instruction.
+  auto issue = [&](int step, WStep &d) {
+    const int ka = step * 8 + kq, kb = ka + 4;
+    d.t0 = (uok && ka < K4) ? wt[ka] : uint4{0, 0, 0, 0};
+    d.t1 = (uok && kb < K4) ? wt[kb] : uint4{0, 0, 0, 0};
   };
 
-  for (int c0 = 0; c0 < cnt; c0 += 16) {
-    const int m = lane & 15;
-    const bool rvalid = c0 + m < cnt;
-    int64_t src_row = 0;
-    if (rvalid) src_row = perm[p0 + c0 + m] / p.a_row_div;
+  for (int c0 = 0; c0 < cnt; c0 += RC) {
+    const int rows = min(RC, cnt - c0);
+    WStep b0, b1, b2;
+    // The weight stream does not depend on the rows: start it first.
+    issue(0, b0);
+    if (1 < steps) issue(1, b1);
 
-    floatx4 tot[NARR][4], tmp[NARR][4];
+    // Stage this chunk's A rows (gathered through perm) in LDS.
+    for (int r = wave; r < RC; r += 4) {
+      const bool ok = r < rows;
+      const int64_t src = ok ? perm[p0 + c0 + r] / p.a_row_div : 0;
+      const AT *xr = abase + src * p.K;
+      for (int k = lane * 4; k < kp; k += WAVE * 4) {
+        half4 h, l;
 #pragma unroll
-    for (int a = 0; a < NARR; a++)
+        for (int j = 0; j < 4; j++) {
+          const float v = (ok && k + j < p.K) ? (float)xr[k + j] : 0.f;
+          const _Float16 hv = (_Float16)v;
+          h[j] = hv;
+          l[j] = (_Float16)(v - (float)hv);
+        }
+        *(half4 *)(ahi + r * kp + k) = h;
+        if (SPLIT) *(half4 *)(alo + r * kp + k) = l;
+      }
+    }
+    __syncthreads();
+
+    floatx4 tot[4], tmp[GROUPED ? 4 : 1];
+#pragma unroll
+    for (int i = 0; i < 4; i++) tot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < (GROUPED ? 4 : 1); i++) tmp[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int ar = m < rows ? m : 0;  // rows past the chunk read row 0, masked below
+    const bool rok = m < rows;
+
+    auto compute = [&](int step, const WStep &d) {
+      half8 a_hi = a_frag(ahi, kp, ar, step, kq);
+      half8 a_lo;
+      if (SPLIT) a_lo = a_frag(alo, kp, ar, step, kq);
+      if (!rok) {
+        a_hi = half8{};
+        if (SPLIT) a_lo = half8{};
+      }
+      floatx4 *acc = GROUPED ? tmp : tot;
+      const uint32_t w0[4] = {d.t0.x, d.t0.y, d.t0.z, d.t0.w};
+      const uint32_t w1[4] = {d.t1.x, d.t1.y, d.t1.z, d.t1.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        tot[a][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-        tmp[a][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const half8 bv = cvt_i8x8(w0[i], w1[i]);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bv, acc[i], 0, 0, 0);
+        if (SPLIT) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, bv, acc[i], 0, 0, 0);
       }
-
-    // Double-buffered: the next step's weight tiles are in flight while the
-    // current step's MFMAs run.
-    WTiles<NARR> cur, nxt;
-    if (sb < se) load_w(sb, nxt);
-    for (int step = sb; step < se; step++) {
-      cur = nxt;
-      if (step + 1 < se) load_w(step + 1, nxt);
-      const int k0 = step * 32 + kq * 8;
-      half8 ahi, alo;
-      AFrag<AT>::load(abase, src_row, p.K, k0, rvalid, ahi, alo);
-#pragma unroll
-      for (int a = 0; a < NARR; a++) {
-        half8 b0v = cvt_i8x8(cur.t0[a].x, cur.t1[a].x);
-        half8 b1v = cvt_i8x8(cur.t0[a].y, cur.t1[a].y);
-        half8 b2v = cvt_i8x8(cur.t0[a].z, cur.t1[a].z);
-        half8 b3v = cvt_i8x8(cur.t0[a].w, cur.t1[a].w);
-        tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b0v, tmp[a][0], 0, 0, 0);
-        tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b1v, tmp[a][1], 0, 0, 0);
-        tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b2v, tmp[a][2], 0, 0, 0);
-        tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b3v, tmp[a][3], 0, 0, 0);
-        if (AFrag<AT>::SPLIT) {
-          tmp[a][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b0v, tmp[a][0], 0, 0, 0);
-          tmp[a][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b1v, tmp[a][1], 0, 0, 0);
-          tmp[a][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b2v, tmp[a][2], 0, 0, 0);
-          tmp[a][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b3v, tmp[a][3], 0, 0, 0);
-        }
-      }
-      // Fold the group's partial sums with its scales at each group end and
-      // at the end of this wavefront's K range.
-      const int kend = min(p.K, (step + 1) * 32);
-      if (kend % p.g == 0 || step == se - 1) {
-        const int grp = (step * 32) / p.g;
-#pragma unroll
-        for (int a = 0; a < NARR; a++) {
-          const float *sc = (a == 0) ? s0 : s1;
+      if (GROUPED) {
+        // Fold the group's partial sums with its scales at each group end.
+        const int kend = min(p.K, (step + 1) * 32);
+        if (kend % p.g == 0 || step == steps - 1) {
+          const int grp = (step * 32) / p.g;
           floatx4 s4 = uok ? *(const floatx4 *)(sc + ((int64_t)e * kg + grp) * p.N + 4 * u)
                            : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            tot[a][i] += tmp[a][i] * s4[i];
-            tmp[a][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            tot[i] += tmp[i] * s4[i];
+            tmp[i] = floatx4{0.f, 0.f, 0.f, 0.f};
           }
         }
       }
+    };
+
+    // Buffers rotate b0 → b1 → b2; every phase is guarded, no early exits.
+    for (int step = 0; step < steps; step += 3) {
+      if (step + 2 < steps) issue(step + 2, b2);
+      compute(step, b0);
+      if (step + 1 < steps) {
+        if (step + 3 < steps) issue(step + 3, b0);
+        compute(step + 1, b1);
+      }
+      if (step + 2 < steps) {
+        if (step + 4 < steps) issue(step + 4, b1);
+        compute(step + 2, b2);
+      }
+    }
+    // tot[i][q]: row 4·kq + q of the chunk, column 4·u + i; scale and bias.
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (!GROUPED) tot[i] = tot[i] * s_one[i];
+      tot[i] += bias4[i];
     }
 
-    __syncthreads();
+    if (MODE == MODE_UP) {
+      __syncthreads();  // every wavefront is done with the staged A
+      if (arr == 1) {
 #pragma unroll
-    for (int a = 0; a < NARR; a++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) red[wave][a * 4 + i][lane] = tot[a][i];
-    __syncthreads();
-
-    // Wavefront i finishes column i of every unit: C row 4·kq + q, unit u.
-    {
-      const int i = wave;
-      floatx4 sum[NARR];
-#pragma unroll
-      for (int a = 0; a < NARR; a++) {
-        sum[a] = red[0][a * 4 + i][lane];
-        sum[a] += red[1][a * 4 + i][lane];
-        sum[a] += red[2][a * 4 + i][lane];
-        sum[a] += red[3][a * 4 + i][lane];
+        for (int i = 0; i < 4; i++) red[(cg * 4 + i) * WAVE + lane] = tot[i];
       }
-      if (uok) {
-        const int n = 4 * u + i;
-        const float bias0 = b0 ? b0[(int64_t)e * p.N + n] : 0.f;
-        const float bias1 = b1 ? b1[(int64_t)e * p.N + n] : 0.f;
+      __syncthreads();
+      if (arr == 0 && uok) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int mm = kq * 4 + q;
-          if (c0 + mm < cnt) {
-            const int64_t asg = perm[p0 + c0 + mm];
-            float v;
-            if (MODE == MODE_UP)
-              v = swiglu(sum[0][q] + bias0, sum[NARR - 1][q] + bias1);
-            else
-              v = sum[0][q] + bias0;
-            out[asg * p.N + n] = v;
+        for (int i = 0; i < 4; i++) {
+          const floatx4 lin = red[(cg * 4 + i) * WAVE + lane];
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int mm = kq * 4 + q;
+            if (mm < rows)
+              out[(int64_t)perm[p0 + c0 + mm] * p.N + 4 * u + i] = swiglu(tot[i][q], lin[q]);
           }
         }
       }
+    } else if (uok) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int mm = kq * 4 + q;
+        if (mm < rows) {
+          floatx4 v = {tot[0][q], tot[1][q], tot[2][q], tot[3][q]};
+          *(floatx4 *)(out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * u) = v;
+        }
+      }
     }
+    __syncthreads();
   }
+}
+
+// Rows staged per chunk: no more than the rows an expert can get from T
+// tokens with distinct ids per token (more rows only take more chunks), and
+// at most what 64 KB of LDS holds.
+int skinny_rows(int K, bool split, int T) {
+  int r = 1;
+  while (r < T && r < 16) r <<= 1;
+  const int cap = a_stage_rows(K, split);
+  return r < cap ? r : cap;
+}
+
+// LDS bytes of k_expert_skinny: the staged A, or the reduction buffer when
+// that is larger (they share the bytes).
+size_t skinny_lds_bytes(int K, bool split, int rc) {
+  const size_t a = (size_t)rc * a_stage_kp(K) * 2 * (split ? 2 : 1);
+  const size_t r = 2 * 4 * WAVE * sizeof(floatx4);
+  return a > r ? a : r;
 }
 
 __device__ __forceinline__ int route_expert(const float *route, int64_t a, int k, int E) {
@@ -369,11 +420,24 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
   const bool mfma = ea.bits == 8 && (ea.g == ea.K || ea.g % 32 == 0);
   const int max_active = ea.E < ea.A ? ea.E : ea.A;
   if (mfma) {
-    dim3 grid((ea.N / 4 + 15) / 16, max_active, ea.calls), block(256);
-    if (ea.a_dtype == MOE_F16)
-      hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16>), grid, block, 0, s, p);
-    else
-      hipLaunchKernelGGL((k_expert_skinny<MODE, float>), grid, block, 0, s, p);
+    const int cgb = MODE == MODE_UP ? 2 : 4;  // column groups of 64 per block
+    dim3 grid(((ea.N / 4 + 15) / 16 + cgb - 1) / cgb, max_active, ea.calls), block(256);
+    const bool grouped = ea.g != ea.K;
+    const bool split = ea.a_dtype != MOE_F16;
+    ExpertKArgs q = p;
+    q.rc = skinny_rows(ea.K, split, ea.A / ea.k);
+    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc);
+    if (!split) {
+      if (grouped)
+        hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16, true>), grid, block, lds, s, q);
+      else
+        hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16, false>), grid, block, lds, s, q);
+    } else {
+      if (grouped)
+        hipLaunchKernelGGL((k_expert_skinny<MODE, float, true>), grid, block, lds, s, q);
+      else
+        hipLaunchKernelGGL((k_expert_skinny<MODE, float, false>), grid, block, lds, s, q);
+    }
   } else {
     dim3 grid(ea.A, (ea.N + 255) / 256, ea.calls), block(256);
     if (ea.a_dtype == MOE_F16)

@@ -222,7 +222,7 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   size_t o_base = p.take(sizeof(int32_t) * C * nblk * E);
   size_t o_off = p.take(sizeof(int32_t) * C * (E + 1));
   size_t o_toff = p.take(sizeof(int32_t) * C * (E + 1));
-  size_t o_act_list = p.take(sizeof(int32_t) * C * E);
+  size_t o_act_list = p.take(sizeof(int32_t) * C * 4 * E);
   size_t o_meta = p.take(sizeof(int32_t) * C * META_N);
   size_t o_perm = p.take(sizeof(int32_t) * C * A);
   size_t o_route = p.take(sizeof(float) * C * route_floats);

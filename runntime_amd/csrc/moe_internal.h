@@ -99,13 +99,14 @@ struct DispatchBufs {
   int32_t *blk_base;    // [nblk, E] per call
   int32_t *offsets;     // [E + 1] per call
   int32_t *tile_off;    // [E + 1] per call: cumulative M-tiles per expert
-  int32_t *active;      // [E] per call: ids of experts with rows, ascending
+  int32_t *active;      // [E][4] per call: {expert, first row, rows, first M-tile} of the
+                        // experts with rows, ascending; then {-1, 0, 0, 0}
   int32_t *meta;        // [META_N] per call
   int32_t *perm;        // [A] per call: sorted position → assignment
   int E, A, nblk;       // sizes that give the per-call strides
   __host__ __device__ int64_t cnt_cs() const { return (int64_t)nblk * E; }
   __host__ __device__ int64_t off_cs() const { return (int64_t)E + 1; }
-  __host__ __device__ int64_t act_cs() const { return E; }
+  __host__ __device__ int64_t act_cs() const { return 4 * (int64_t)E; }
   __host__ __device__ int64_t meta_cs() const { return META_N; }
   __host__ __device__ int64_t perm_cs() const { return A; }
 };

@@ -129,15 +129,26 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   const int et = min(RT_EXPERTS, E - e0);
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
-  for (int i = threadIdx.x; i < RT_TOKENS * ROUTER_CHUNK; i += blockDim.x) {
+  // Staging: every load of the tile is issued before the first LDS store.
+  constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
+  float xv[XPER], wv[WPER];
+#pragma unroll
+  for (int r = 0; r < XPER; r++) {
+    int i = threadIdx.x + 256 * r;
     int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
     int t = t0 + tt;
-    xs[i] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+    xv[r] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
   }
-  for (int i = threadIdx.x; i < ROUTER_CHUNK * RT_EXPERTS; i += blockDim.x) {
+#pragma unroll
+  for (int r = 0; r < WPER; r++) {
+    int i = threadIdx.x + 256 * r;
     int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
-    ws[i] = (kk < len && ee < et) ? w[(int64_t)(k0 + kk) * E + e0 + ee] : 0.f;
+    wv[r] = (kk < len && ee < et) ? w[(int64_t)(k0 + kk) * E + e0 + ee] : 0.f;
   }
+#pragma unroll
+  for (int r = 0; r < XPER; r++) xs[threadIdx.x + 256 * r] = xv[r];
+#pragma unroll
+  for (int r = 0; r < WPER; r++) ws[threadIdx.x + 256 * r] = wv[r];
   __syncthreads();
   for (int p = threadIdx.x; p < RT_TOKENS * RT_EXPERTS; p += blockDim.x) {
     int tt = p / RT_EXPERTS, ee = p % RT_EXPERTS;
