@@ -5,9 +5,12 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]
 Default workload: config 2 (the metric's decode configuration): 1000
 independent single-token layer calls (T=1, d=640, E=128, k=4, I=640, f32
 activations, int8 weights with per-channel scales). One step = the 1000
-calls, issued back to back on one stream and replayed from a HIP graph.
-Call j uses weight copy j mod C, so the expert weights (158 MB per copy) do
-not stay in the 256 MB MALL between calls. Inputs are resident in HBM
+calls, enqueued as moe_layer_batched launches of W calls each (default: all
+1000 in one) and replayed from a HIP graph. Every call has its own copy of
+the layer's weights (158 MB each), so no call can reuse another's expert
+bytes from L2 or the 256 MB MALL: each token's experts really stream from
+HBM. The launch-bound figure — the same 1000 calls one at a time — is
+reported beside it as sequential_tokens_per_s. Inputs are resident in HBM
 before the timed region. Prints one JSON line.
 """
 import argparse
@@ -162,7 +165,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--copies", type=int, default=2, help="rotating input sets (config 3)")
-    ap.add_argument("--calls-per-launch", type=int, default=100,
+    ap.add_argument("--calls-per-launch", type=int, default=1000,
                     help="config 2: independent single-token calls per batched launch")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)

@@ -23,6 +23,8 @@
 //
 // k_expert_simple — VALU fallback for every other case (int4, small
 // groups): one thread per (row, column), f32 fma per group, then × scale.
+#include <stdlib.h>
+
 #include "moe_internal.h"
 
 namespace {
@@ -123,27 +125,40 @@ struct WStep {
   uint4 t0, t1;
 };
 
-// k_expert_skinny: one block = one active expert × CGB groups of 64 output
-// columns (16 quantW units each). The expert's rows are taken RC at a time
-// (RC ≤ 16 keeps them in LDS); for each chunk the block stages the rows' A in
-// LDS once, then each wavefront streams one weight array for one column
-// group over the whole of K (up: {glu, lin} × 2 groups; down: 4 groups)
-// through a 3-stage register pipeline: the weight loads of steps s+1 and s+2
-// are in flight while step s converts and multiplies. A comes from LDS, so
-// its reads never wait behind the weight stream; scales and biases are
-// fetched before the stream starts. Up's glu and lin wavefronts meet in LDS
-// for the SwiGLU epilogue.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Weight tiles are read with plain loads: the 4 lanes of a unit read half
+// of a 128-byte line per instruction and the next instruction reads the
+// other half, which then comes from L2. (Nontemporal loads refetch it: on
+// MI355X they made this kernel ~25% slower, though they stream whole lines
+// faster than plain loads.)
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) { return *p; }
+
+// k_expert_skinny: one block = one active expert × NW·(column groups per
+// wavefront) groups of 64 output columns (16 quantW units each). The
+// expert's rows are taken RC at a time (RC ≤ 16 keeps them in LDS); for each
+// chunk the NW wavefronts stage the rows' A in LDS once, then each wavefront
+// streams its segments — up: glu then lin of one column group; down: NS
+// column groups — as one continuous stream over K through a 4-stage register
+// pipeline: the loads of steps g+1..g+3 are in flight while step g converts
+// and multiplies. A comes from LDS, so its reads never wait behind the weight
+// stream; scales and biases are fetched before the stream starts. The glu
+// sums wait in LDS for the SwiGLU epilogue.
 // GROUPED: scales change along K (groupSize < K), so partial sums are
 // scaled per group; otherwise one scale per column is applied at the end.
-template <int MODE, typename AT, bool GROUPED>
-__global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
-  constexpr int NARR = (MODE == MODE_UP) ? 2 : 1;
-  constexpr int CGB = 4 / NARR;  // column groups per block
+template <int MODE, typename AT, bool GROUPED, int NW, int NS>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_skinny(
+    ExpertKArgs p) {
+  // Up with NS = 2: one wavefront streams glu then lin of its column group.
+  // Up with NS = 1: glu and lin on paired wavefronts (2w, 2w+1), which meet
+  // in LDS after the stream. Down: NS column groups per wavefront.
+  constexpr bool PAIRED = MODE == MODE_UP && NS == 1;
+  static_assert(!PAIRED || NW % 2 == 0, "paired up needs an even wavefront count");
+  constexpr int GPW = (MODE == MODE_UP) ? 1 : NS;  // column groups per wavefront
   constexpr bool SPLIT = AStage<AT>::SPLIT;
-  // LDS: the staged A rows during the K loop, then (same bytes) the lin
-  // wavefronts' sums [CGB][4][64] floatx4 for the up epilogue.
+  // LDS: the staged A rows, then each wavefront's parked glu sums
+  // [NW][4][64] floatx4 (up only).
   extern __shared__ __align__(16) unsigned char smem[];
-  floatx4 *red = (floatx4 *)smem;
   _Float16 *ahi = (_Float16 *)smem;
 
   const int call = blockIdx.z;
@@ -157,47 +172,67 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
 
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
-  const int arr = wave % NARR;  // weight array of this wavefront
-  const int cg = wave / NARR;   // column group of this wavefront
   const int N4 = p.N / 4, K4 = p.K / 4;
-  const int u = (blockIdx.x * CGB + cg) * 16 + (lane & 15);
-  const bool uok = u < N4;
+  const int arr = PAIRED ? (wave & 1) : 0;  // weight array of a paired wavefront
+  const int cg0 = PAIRED ? blockIdx.x * (NW / 2) + (wave >> 1)
+                         : (blockIdx.x * NW + wave) * GPW;  // first column group
+  int useg[NS];
+  bool uok[NS];
+#pragma unroll
+  for (int j = 0; j < NS; j++) {
+    useg[j] = (cg0 + (MODE == MODE_UP ? 0 : j)) * 16 + (lane & 15);
+    uok[j] = useg[j] < N4;
+  }
   const int kq = lane >> 4;
   const int m = lane & 15;
   const int steps = (p.K + 31) / 32;
+  const int gsteps = NS * steps;
   const int kg = p.K / p.g;
   const int kp = a_stage_kp(p.K);
   const int RC = p.rc;
+  const int planes = SPLIT ? 2 : 1;
   _Float16 *alo = ahi + RC * kp;
+  floatx4 *park = (floatx4 *)(smem + (size_t)RC * kp * 2 * planes) +
+                  (PAIRED ? (wave >> 1) : wave) * 4 * WAVE;
 
-  const uint32_t *wbase = arr == 0 ? p.w0 + call * p.w0_cs : p.w1 + call * p.w1_cs;
-  const float *sc = arr == 0 ? p.s0 + call * p.s0_cs : p.s1 + call * p.s1_cs;
-  const float *bp = arr == 0 ? (p.b0 ? p.b0 + call * p.b0_cs : nullptr)
-                             : (p.b1 ? p.b1 + call * p.b1_cs : nullptr);
-  const uint4 *wt = (const uint4 *)wbase + ((int64_t)e * N4 + (uok ? u : 0)) * K4;
-  // This wavefront's 4 columns: scales (one group) and biases, fetched early.
-  const floatx4 s_one = (!GROUPED && uok) ? *(const floatx4 *)(sc + (int64_t)e * p.N + 4 * u)
-                                           : floatx4{0.f, 0.f, 0.f, 0.f};
-  const floatx4 bias4 = (bp && uok) ? *(const floatx4 *)(bp + (int64_t)e * p.N + 4 * u)
-                                    : floatx4{0.f, 0.f, 0.f, 0.f};
+  const uint4 *wt[NS];
+  const float *sc[NS];
+  floatx4 sone[NS], bias[NS];
+#pragma unroll
+  for (int j = 0; j < NS; j++) {
+    const bool second = MODE == MODE_UP && (PAIRED ? arr == 1 : j == 1);
+    const uint32_t *w = second ? p.w1 + call * p.w1_cs : p.w0 + call * p.w0_cs;
+    sc[j] = second ? p.s1 + call * p.s1_cs : p.s0 + call * p.s0_cs;
+    const float *b = second ? (p.b1 ? p.b1 + call * p.b1_cs : nullptr)
+                            : (p.b0 ? p.b0 + call * p.b0_cs : nullptr);
+    wt[j] = (const uint4 *)w + ((int64_t)e * N4 + (uok[j] ? useg[j] : 0)) * K4;
+    // This segment's 4 columns: scales (one group) and biases, fetched early.
+    sone[j] = (!GROUPED && uok[j]) ? *(const floatx4 *)(sc[j] + (int64_t)e * p.N + 4 * useg[j])
+                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+    bias[j] = (b && uok[j]) ? *(const floatx4 *)(b + (int64_t)e * p.N + 4 * useg[j])
+                            : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
 
-  // Tiles 8·step + kq and 8·step + 4 + kq: the 4 lanes of a unit read 64
-  // contiguous bytes per load instruction.
-  auto issue = [&](int step, WStep &d) {
-    const int ka = step * 8 + kq, kb = ka + 4;
-    d.t0 = (uok && ka < K4) ? wt[ka] : uint4{0, 0, 0, 0};
-    d.t1 = (uok && kb < K4) ? wt[kb] : uint4{0, 0, 0, 0};
+  // Stream step g = seg·steps + s: tiles 8·s + kq and 8·s + 4 + kq of the
+  // segment; the 4 lanes of a unit read 64 contiguous bytes per load.
+  auto issue = [&](int g, WStep &d) {
+    const int seg = NS == 1 ? 0 : (g >= steps ? 1 : 0);
+    const int s = g - seg * steps;
+    const int ka = s * 8 + kq, kb = ka + 4;
+    d.t0 = (uok[seg] && ka < K4) ? load_stream(wt[seg] + ka) : uint4{0, 0, 0, 0};
+    d.t1 = (uok[seg] && kb < K4) ? load_stream(wt[seg] + kb) : uint4{0, 0, 0, 0};
   };
 
   for (int c0 = 0; c0 < cnt; c0 += RC) {
     const int rows = min(RC, cnt - c0);
-    WStep b0, b1, b2;
+    WStep b0, b1, b2, b3;
     // The weight stream does not depend on the rows: start it first.
     issue(0, b0);
-    if (1 < steps) issue(1, b1);
+    if (1 < gsteps) issue(1, b1);
+    if (2 < gsteps) issue(2, b2);
 
     // Stage this chunk's A rows (gathered through perm) in LDS.
-    for (int r = wave; r < RC; r += 4) {
+    for (int r = wave; r < RC; r += NW) {
       const bool ok = r < rows;
       const int64_t src = ok ? perm[p0 + c0 + r] / p.a_row_div : 0;
       const AT *xr = abase + src * p.K;
@@ -224,10 +259,49 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
     const int ar = m < rows ? m : 0;  // rows past the chunk read row 0, masked below
     const bool rok = m < rows;
 
-    auto compute = [&](int step, const WStep &d) {
-      half8 a_hi = a_frag(ahi, kp, ar, step, kq);
+    // tot[i][q]: row 4·kq + q of the chunk, column 4·useg + i.
+    auto finish = [&](int seg) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (!GROUPED) tot[i] = tot[i] * sone[seg][i];
+        tot[i] += bias[seg][i];
+      }
+      if (PAIRED) return;  // the SwiGLU runs after the stream, with the partner
+      if (MODE == MODE_UP && seg == 0) {
+        // Park glu; the wavefront reads its own lanes back, no barrier.
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          park[i * WAVE + lane] = tot[i];
+          tot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+        return;
+      }
+      if (uok[seg]) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int mm = kq * 4 + q;
+          if (mm >= rows) continue;
+          float *orow = out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * useg[seg];
+          floatx4 v;
+          if (MODE == MODE_UP) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = swiglu(park[i * WAVE + lane][q], tot[i][q]);
+          } else {
+            v = floatx4{tot[0][q], tot[1][q], tot[2][q], tot[3][q]};
+          }
+          *(floatx4 *)orow = v;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) tot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    auto compute = [&](int g, const WStep &d) {
+      const int seg = NS == 1 ? 0 : (g >= steps ? 1 : 0);
+      const int s = g - seg * steps;
+      half8 a_hi = a_frag(ahi, kp, ar, s, kq);
       half8 a_lo;
-      if (SPLIT) a_lo = a_frag(alo, kp, ar, step, kq);
+      if (SPLIT) a_lo = a_frag(alo, kp, ar, s, kq);
       if (!rok) {
         a_hi = half8{};
         if (SPLIT) a_lo = half8{};
@@ -243,11 +317,12 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
       }
       if (GROUPED) {
         // Fold the group's partial sums with its scales at each group end.
-        const int kend = min(p.K, (step + 1) * 32);
-        if (kend % p.g == 0 || step == steps - 1) {
-          const int grp = (step * 32) / p.g;
-          floatx4 s4 = uok ? *(const floatx4 *)(sc + ((int64_t)e * kg + grp) * p.N + 4 * u)
-                           : floatx4{0.f, 0.f, 0.f, 0.f};
+        const int kend = min(p.K, (s + 1) * 32);
+        if (kend % p.g == 0 || s == steps - 1) {
+          const int grp = (s * 32) / p.g;
+          floatx4 s4 = uok[seg] ? *(const floatx4 *)(sc[seg] + ((int64_t)e * kg + grp) * p.N +
+                                                      4 * useg[seg])
+                                : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             tot[i] += tmp[i] * s4[i];
@@ -255,58 +330,48 @@ __global__ __launch_bounds__(256) void k_expert_skinny(ExpertKArgs p) {
           }
         }
       }
+      if (s == steps - 1) finish(seg);
     };
 
-    // Buffers rotate b0 → b1 → b2; every phase is guarded, no early exits.
-    for (int step = 0; step < steps; step += 3) {
-      if (step + 2 < steps) issue(step + 2, b2);
-      compute(step, b0);
-      if (step + 1 < steps) {
-        if (step + 3 < steps) issue(step + 3, b0);
-        compute(step + 1, b1);
+    // Buffers rotate b0 → b1 → b2 → b3 (loads three steps ahead); every
+    // phase is guarded, no early exits.
+    for (int g = 0; g < gsteps; g += 4) {
+      if (g + 3 < gsteps) issue(g + 3, b3);
+      compute(g, b0);
+      if (g + 1 < gsteps) {
+        if (g + 4 < gsteps) issue(g + 4, b0);
+        compute(g + 1, b1);
       }
-      if (step + 2 < steps) {
-        if (step + 4 < steps) issue(step + 4, b1);
-        compute(step + 2, b2);
+      if (g + 2 < gsteps) {
+        if (g + 5 < gsteps) issue(g + 5, b1);
+        compute(g + 2, b2);
+      }
+      if (g + 3 < gsteps) {
+        if (g + 6 < gsteps) issue(g + 6, b2);
+        compute(g + 3, b3);
       }
     }
-    // tot[i][q]: row 4·kq + q of the chunk, column 4·u + i; scale and bias.
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      if (!GROUPED) tot[i] = tot[i] * s_one[i];
-      tot[i] += bias4[i];
-    }
-
-    if (MODE == MODE_UP) {
-      __syncthreads();  // every wavefront is done with the staged A
+    if (PAIRED) {
+      // lin wavefront parks its sums; glu wavefront applies the SwiGLU.
       if (arr == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) red[(cg * 4 + i) * WAVE + lane] = tot[i];
+        for (int i = 0; i < 4; i++) park[i * WAVE + lane] = tot[i];
       }
       __syncthreads();
-      if (arr == 0 && uok) {
+      if (arr == 0 && uok[0]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const floatx4 lin = red[(cg * 4 + i) * WAVE + lane];
+        for (int q = 0; q < 4; q++) {
+          const int mm = kq * 4 + q;
+          if (mm >= rows) continue;
+          float *orow = out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * useg[0];
+          floatx4 v;
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int mm = kq * 4 + q;
-            if (mm < rows)
-              out[(int64_t)perm[p0 + c0 + mm] * p.N + 4 * u + i] = swiglu(tot[i][q], lin[q]);
-          }
-        }
-      }
-    } else if (uok) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int mm = kq * 4 + q;
-        if (mm < rows) {
-          floatx4 v = {tot[0][q], tot[1][q], tot[2][q], tot[3][q]};
-          *(floatx4 *)(out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * u) = v;
+          for (int i = 0; i < 4; i++) v[i] = swiglu(tot[i][q], park[i * WAVE + lane][q]);
+          *(floatx4 *)orow = v;
         }
       }
     }
-    __syncthreads();
+    __syncthreads();  // the next chunk restages A
   }
 }
 
@@ -320,12 +385,9 @@ int skinny_rows(int K, bool split, int T) {
   return r < cap ? r : cap;
 }
 
-// LDS bytes of k_expert_skinny: the staged A, or the reduction buffer when
-// that is larger (they share the bytes).
-size_t skinny_lds_bytes(int K, bool split, int rc) {
-  const size_t a = (size_t)rc * a_stage_kp(K) * 2 * (split ? 2 : 1);
-  const size_t r = 2 * 4 * WAVE * sizeof(floatx4);
-  return a > r ? a : r;
+// LDS bytes of k_expert_skinny: the staged A and (up) the parked glu sums.
+size_t skinny_lds_bytes(int K, bool split, int rc, int parks) {
+  return (size_t)rc * a_stage_kp(K) * 2 * (split ? 2 : 1) + (size_t)parks * 4 * WAVE * sizeof(floatx4);
 }
 
 __device__ __forceinline__ int route_expert(const float *route, int64_t a, int k, int E) {
@@ -420,24 +482,47 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
   const bool mfma = ea.bits == 8 && (ea.g == ea.K || ea.g % 32 == 0);
   const int max_active = ea.E < ea.A ? ea.E : ea.A;
   if (mfma) {
-    const int cgb = MODE == MODE_UP ? 2 : 4;  // column groups of 64 per block
-    dim3 grid(((ea.N / 4 + 15) / 16 + cgb - 1) / cgb, max_active, ea.calls), block(256);
-    const bool grouped = ea.g != ea.K;
-    const bool split = ea.a_dtype != MOE_F16;
     ExpertKArgs q = p;
+    const bool split = ea.a_dtype != MOE_F16;
+    const bool grouped = ea.g != ea.K;
     q.rc = skinny_rows(ea.K, split, ea.A / ea.k);
-    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc);
+    // Wavefronts per block: enough to share the staged A so it costs at most
+    // ~8 KB of LDS per wavefront. Column groups per wavefront (down): 2 for
+    // longer weight streams when that still leaves ≥ 2 wavefronts per SIMD.
+    const size_t a_bytes = (size_t)q.rc * a_stage_kp(ea.K) * 2 * (split ? 2 : 1);
+    int nw = a_bytes <= 8192 ? 1 : a_bytes <= 16384 ? 2 : 4;
+    const int ncg = (ea.N / 4 + 15) / 16;
+    // Longer streams (NS = 2) while they still give ≥ 2 wavefronts per SIMD.
+    const long waves_ns2 = (long)ea.calls * max_active * (MODE == MODE_UP ? ncg : (ncg + 1) / 2);
+    int ns = waves_ns2 >= 2048 ? 2 : 1;
+    // Tuning overrides (MOE_SKINNY_NS = 1|2, MOE_SKINNY_NW = 1|2|4).
+    static const int env_ns = getenv("MOE_SKINNY_NS") ? atoi(getenv("MOE_SKINNY_NS")) : 0;
+    static const int env_nw = getenv("MOE_SKINNY_NW") ? atoi(getenv("MOE_SKINNY_NW")) : 0;
+    if (env_ns == 1 || env_ns == 2) ns = env_ns;
+    if (env_nw == 1 || env_nw == 2 || env_nw == 4) nw = env_nw;
+    if (MODE == MODE_UP && ns == 1 && nw == 1) nw = 2;  // glu/lin pairs
+    const int gpw = (MODE == MODE_UP) ? 1 : ns;
+    const int cg_per_block = (MODE == MODE_UP && ns == 1) ? nw / 2 : nw * gpw;
+    dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw);
+    // Up parks one [4][64] floatx4 per wavefront (per pair when paired).
+    const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
+    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks);
+#define SKINNY(AT_, GR_, NW_, NS_)                                                        \
+  hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_>), grid, block, lds, s, q)
+#define SKINNY_NS(AT_, GR_, NW_)                                                          \
+  if (ns == 2) { SKINNY(AT_, GR_, NW_, 2); }                                              \
+  else if constexpr (MODE == MODE_DOWN || NW_ % 2 == 0) { SKINNY(AT_, GR_, NW_, 1); }
+#define SKINNY_NW(AT_, GR_)                                                               \
+  if (nw == 1) { SKINNY_NS(AT_, GR_, 1); } else if (nw == 2) { SKINNY_NS(AT_, GR_, 2); }  \
+  else { SKINNY_NS(AT_, GR_, 4); }
     if (!split) {
-      if (grouped)
-        hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16, true>), grid, block, lds, s, q);
-      else
-        hipLaunchKernelGGL((k_expert_skinny<MODE, _Float16, false>), grid, block, lds, s, q);
+      if (grouped) { SKINNY_NW(_Float16, true); } else { SKINNY_NW(_Float16, false); }
     } else {
-      if (grouped)
-        hipLaunchKernelGGL((k_expert_skinny<MODE, float, true>), grid, block, lds, s, q);
-      else
-        hipLaunchKernelGGL((k_expert_skinny<MODE, float, false>), grid, block, lds, s, q);
+      if (grouped) { SKINNY_NW(float, true); } else { SKINNY_NW(float, false); }
     }
+#undef SKINNY_NW
+#undef SKINNY_NS
+#undef SKINNY
   } else {
     dim3 grid(ea.A, (ea.N + 255) / 256, ea.calls), block(256);
     if (ea.a_dtype == MOE_F16)

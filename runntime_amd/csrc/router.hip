@@ -143,7 +143,8 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   for (int r = 0; r < WPER; r++) {
     int i = threadIdx.x + 256 * r;
     int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
-    wv[r] = (kk < len && ee < et) ? w[(int64_t)(k0 + kk) * E + e0 + ee] : 0.f;
+    wv[r] = (kk < len && ee < et) ? __builtin_nontemporal_load(w + (int64_t)(k0 + kk) * E + e0 + ee)
+                                  : 0.f;
   }
 #pragma unroll
   for (int r = 0; r < XPER; r++) xs[threadIdx.x + 256 * r] = xv[r];

@@ -150,9 +150,15 @@ def make_weight_copies(cfg: MoeConfig, copies: int, seed: int = 0,
     C, E, d, I = copies, cfg.E, cfg.d, cfg.I
 
     def ew(K, N):
-        q = torch.randint(-127, 128, (C * E, K, N), generator=g, dtype=torch.int8, device=device)
-        words = pack_expert_weights_torch(q).view(C, -1)
-        del q
+        # Drawn and packed 16 copies at a time into the final tensor, so the
+        # int8 draw and its packed copy never both exist for all copies.
+        words = torch.empty((C, E * K * N // 4), dtype=torch.int32, device=device)
+        for c0 in range(0, C, 16):
+            c1 = min(C, c0 + 16)
+            q = torch.randint(-127, 128, ((c1 - c0) * E, K, N), generator=g, dtype=torch.int8,
+                              device=device)
+            words[c0:c1] = pack_expert_weights_torch(q).view(c1 - c0, -1)
+            del q
         sc = torch.rand((C, E, N), generator=g, dtype=torch.float32, device=device) * 1.5e-3 + 0.5e-3
         return QuantExpertWeight(QuantW(words, (E * K, N)), sc,
                                  torch.zeros((C, E, N), dtype=torch.float32, device=device))
