@@ -551,6 +551,11 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   MOE_NONNULL(db.meta);
   if (db.E != ea.E || db.A != ea.A)
     return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch workspace sized for another shape");
+  // Prefill shapes (≥ 64 rows per expert on average): the grouped GEMM.
+  static const int env_gemm = getenv("MOE_GEMM") ? atoi(getenv("MOE_GEMM")) : -1;
+  const int max_active = ea.E < ea.A ? ea.E : ea.A;
+  const bool want_gemm = env_gemm >= 0 ? env_gemm != 0 : ea.A >= 64 * max_active;
+  if (ea.calls == 1 && want_gemm && gemm_eligible(ea)) return launch_expert_gemm(ea, db, s);
   ExpertKArgs p;
   p.a = ea.a;
   p.a_cs = ea.a_cs;

@@ -249,7 +249,7 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   return MOE_OK;
 }
 
-static constexpr int TILE_M = 128;
+static constexpr int TILE_M = GEMM_TILE_M;
 
 static int after_launch(const char *op) {
   hipError_t e = hipGetLastError();

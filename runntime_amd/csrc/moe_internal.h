@@ -91,6 +91,8 @@ enum MetaSlot { META_VALID = 0, META_ACTIVE = 1, META_MAXCNT = 2, META_TILES = 3
 
 // Largest token count whose routing and dispatch one block does (fused).
 constexpr int SMALL_T = 16;
+// Rows per M-tile of the grouped GEMM; the dispatch counts M-tiles with it.
+constexpr int GEMM_TILE_M = 128;
 
 // Dispatch workspace of a batch of calls. Each call owns a slice: the
 // per-call sizes below are the strides between them.
@@ -168,6 +170,9 @@ struct ExpertArgs {
 };
 
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
+// The grouped GEMM (gemm.hip) for many rows per expert.
+bool gemm_eligible(const ExpertArgs &ea);
+int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 // Fills n floats with 0 (a kernel, not hipMemsetAsync, so a captured graph
 // replays it correctly).
 int launch_zero(float *p, size_t n, hipStream_t s);

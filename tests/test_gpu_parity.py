@@ -216,6 +216,28 @@ def test_moe_down_mfma(shape, k):
     _check_down(T, K, N, E, g, 8, k=k)
 
 
+# Rows per expert ≥ 64 on average: these take the grouped GEMM (128×128
+# tiles). Ragged last M-tiles, grids that are not a multiple of 8 blocks,
+# K not a multiple of 128.
+GEMM_SHAPES = [(300, 128, 256, 4, 128), (260, 192, 128, 3, 192), (1000, 256, 384, 8, 256),
+               (2048, 512, 640, 16, 512)]
+
+
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_moe_up_grouped_gemm(xdtype, shape):
+    T, K, N, E, g = shape
+    say(f"moeUp gemm {xdtype} {shape}")
+    _check_up(T, K, N, E, g, 8, k=2, xdtype=xdtype)
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_moe_down_grouped_gemm(shape):
+    T, K, N, E, g = shape
+    say(f"moeDown gemm {shape}")
+    _check_down(T, K, N, E, g, 8, k=2)
+
+
 def test_moe_up_past_65535_rows():
     T = math.ceil(65535 / 4) + 1
     say(f"moeUp rows={T * 4}")
