@@ -58,6 +58,23 @@ def layer_flops(cfg):
     return 2 * cfg.T * cfg.d * cfg.E + cfg.T * cfg.k * 6 * cfg.d * cfg.I
 
 
+# HBM traffic per launch of the roofline kernel, from the committed
+# FETCH_SIZE / WRITE_SIZE counter passes (calibrated against a plain copy);
+# valid for the default launch shape of each workload.
+TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md"}
+
+
+def profiled_traffic(config, default_shape):
+    name = TRAFFIC_PROFILES.get(config)
+    path = os.path.join(ROOT, "profiles", name) if name else None
+    if not default_shape or path is None or not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), "profiles/" + name
+    return None, None
+
+
 def cpu_baseline(cfg, seconds_budget=15.0):
     """The oracle's f32 restatement of the reference's WGSL kernels
     (topkSelect, moeUp, moeDown; router in the canonical f32 order), timed
@@ -158,6 +175,19 @@ def sequential_rate(cfg, args):
     return n_tok / dt
 
 
+def copy_calibration(mib):
+    """4 launches of a plain copy of `mib` MiB (torch's copy kernel): under
+    rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) each dispatch moves exactly
+    mib MiB each way, which converts the counter's reading to bytes."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n * 4, "launches": 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -171,12 +201,18 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sequential", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
+                    help="only run 4 plain device copies of MiB each (reference reading "
+                         "for the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     cfg = CONFIGS[args.config]
 
     if args.config == 2:
@@ -186,15 +222,15 @@ def main():
         say(f"building {C} input set(s) of {cfg.name}")
         sets = [make_inputs(cfg, seed=200 + c, device="cuda") for c in range(C)]
         out = torch.empty((cfg.T, cfg.d), dtype=torch.float32, device="cuda")
+        route = torch.empty((cfg.T, 2 * cfg.k), dtype=torch.float32, device="cuda")
         perf.reserve(cfg.T, cfg.d, cfg.I, cfg.E, cfg.k)
         counter = [0]
 
         def step():
             for c in range(C):
                 w = sets[c]
-                o = rt.moe_layer(w.x, w.router_w, w.router_b, w.glu, w.lin, w.down, w.residual,
-                                 cfg.k)
-                out.copy_(o)
+                rt.moe_layer(w.x, w.router_w, w.router_b, w.glu, w.lin, w.down, w.residual,
+                             cfg.k, out=out, route=route)
         tokens_per_step = cfg.T * C
 
     stream = torch.cuda.Stream()
@@ -244,11 +280,14 @@ def main():
         calls = tokens_per_step // cfg.T
     up_ms, up_n = groups.get("up", (0.0, 0))
     up_avg_s = up_ms / max(up_n, 1) / 1e3
+    traffic, traffic_src = profiled_traffic(
+        args.config, args.config != 2 or args.calls_per_launch == 1000)
     if args.config in (2, 3):
         per_launch = up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1)
         achieved = per_launch / up_avg_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "traffic_source": traffic_src,
                     "kernel": "k_expert_skinny<up> (gate/up + SwiGLU)",
                     "algorithmic_bytes_per_launch": per_launch,
                     "avg_launch_us": round(up_avg_s * 1e6, 2)}
@@ -258,7 +297,8 @@ def main():
         achieved = fl / up_avg_s / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                    "traffic": None, "kernel": "gate/up grouped GEMM",
+                    "traffic": traffic, "traffic_source": traffic_src,
+                    "kernel": "gate/up grouped GEMM",
                     "algorithmic_flops_per_launch": fl, "avg_launch_us": round(up_avg_s * 1e6, 2)}
         layer_frac = layer_flops(cfg) * calls / (ms_per_step / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS
 

@@ -219,12 +219,14 @@ def moeDown(act, route, out: QuantExpertWeight, residual, opts) -> torch.Tensor:
 
 def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWeight,
               down: QuantExpertWeight, residual, k: int, bits: int = 8,
-              group_size_up=None, group_size_down=None, return_route: bool = False):
+              group_size_up=None, group_size_down=None, return_route: bool = False,
+              out=None, route=None):
     """The routed layer in one call (EagerMoeMlp.forward's quantized branch
     after the norm, zoo/privacy-filter/moeMlp.ts:82-121):
     route = topk(x·Wr + br, k); act = moeUp(x, route, glu, lin);
     out = moeDown(act, route, down, residual). Group sizes default to one
-    scale per output channel (K of each projection)."""
+    scale per output channel (K of each projection). `out` (f32 [T, d]) and
+    `route` (f32 [T, 2k]) may be given to write into existing buffers."""
     t, d, _ = _want2d("moe_layer", x, ("f32", "f16"))
     rw = _dims(router_w)
     if _dtype_name(router_w) != "f32" or len(rw) != 2 or rw[0] != d:
@@ -235,14 +237,21 @@ def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWei
     i = glu.w.dims[1]
     gu = group_size_up or d
     gd = group_size_down or i
-    route = torch.empty((t, 2 * k), dtype=torch.float32, device=x.device)
+    if route is None:
+        route = torch.empty((t, 2 * k), dtype=torch.float32, device=x.device)
+    elif (_dtype_name(route) != "f32" or route.numel() != t * 2 * k
+          or not route.is_contiguous()):
+        raise ValueError(f"moe_layer: route must be contiguous f32 [{t}, {2 * k}]")
     _check_expert_weight("moe_layer", glu, d, route, t, k, {"bits": bits, "groupSize": gu})
     _check_expert_weight("moe_layer", lin, d, route, t, k, {"bits": bits, "groupSize": gu})
     _check_expert_weight("moe_layer", down, i, route, t, k, {"bits": bits, "groupSize": gd})
     if residual is not None and (_dtype_name(residual) != "f32" or residual.numel() != t * d):
         raise ValueError(f"moe_layer: residual must be f32 [{t}, {d}]")
     dev = _device_of(x, router_w, router_b, glu.w, lin.w, down.w, residual)
-    out = torch.empty((t, d), dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty((t, d), dtype=torch.float32, device=dev)
+    elif _dtype_name(out) != "f32" or out.numel() != t * d or not out.is_contiguous():
+        raise ValueError(f"moe_layer: out must be contiguous f32 [{t}, {d}]")
     g, l_, dn = _weight_c(glu), _weight_c(lin), _weight_c(down)
     lib = _lib.load()
     _lib.check(lib.moe_layer(_ctx(dev), x.data_ptr(), _xdtype(x), router_w.data_ptr(),
