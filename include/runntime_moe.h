@@ -182,6 +182,16 @@ MOE_API int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *coun
 MOE_API int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int k, int32_t *perm,
                  int32_t *offsets);
 
+/* Packs E experts' signed int weights into quantW words on the device:
+ * replaces packQuantW (src/core/weights/quantPack.ts:12-28) applied per
+ * expert with the words concatenated expert-major (the upload step of the
+ * weights). ints: device int8 [E][n][k] (each expert output-first, torch's
+ * Linear layout; int4 values in [-8, 7] one per byte). words: device
+ * uint32 [E·k·n·bits/32], the logical [E·k, n] quantW weight. k and n must
+ * be multiples of 4; bits 8 or 4. */
+MOE_API int moe_pack_quantw(moe_ctx *ctx, const int8_t *ints, int E, int k, int n, int bits,
+                            uint32_t *words);
+
 #ifdef __cplusplus
 }
 #endif

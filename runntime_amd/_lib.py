@@ -19,7 +19,7 @@ EXPORTED = (
     "moe_version", "moe_last_error", "moe_ctx_create", "moe_ctx_set_stream",
     "moe_ctx_reserve", "moe_ctx_destroy", "moe_sync", "moe_topk", "moe_router_topk",
     "moe_up", "moe_down", "moe_layer", "moe_dispatch", "moe_prof_enable", "moe_prof_read",
-    "moe_layer_batched", "moe_ctx_reserve_batched",
+    "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine")
 
@@ -68,6 +68,7 @@ def load() -> ctypes.CDLL:
             "moe_down": ([P, P, P, W, P, I, I, I, I, I, I, I, P], I),
             "moe_layer": ([P, P, I, P, P, W, W, W, P, I, I, I, I, I, I, I, I, P, P], I),
             "moe_dispatch": ([P, P, I, I, I, P, P], I),
+            "moe_pack_quantw": ([P, P, I, I, I, I, P], I),
             "moe_prof_enable": ([P, I], I),
             "moe_layer_batched": ([P, I, ctypes.POINTER(CallStridesC), P, I, P, P, W, W, W, P, I,
                                    I, I, I, I, I, I, I, P, P], I),

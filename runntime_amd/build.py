@@ -26,7 +26,7 @@ COMMON = [
 PER_FILE = {
     "router.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip"]
+SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "pack.hip"]
 
 
 def _compile(src: str) -> str:

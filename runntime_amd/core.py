@@ -261,6 +261,22 @@ def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWei
     return (out, route) if return_route else out
 
 
+def pack_quant_w_device(ints: torch.Tensor, bits: int = 8) -> QuantW:
+    """packQuantW (src/core/weights/quantPack.ts:12-28) on the device for a
+    whole layer: `ints` is int8 [E, n, k] (each expert output-first, torch's
+    Linear layout) or [n, k] for one expert, on the GPU. Returns the quantW
+    weight of logical dims [E·k, n] (experts concatenated expert-major)."""
+    if ints.dtype != torch.int8 or ints.dim() not in (2, 3) or not ints.is_cuda:
+        raise ValueError("packQuantW: ints must be a device int8 [E, n, k] or [n, k] tensor")
+    e, n, k = (1, *ints.shape) if ints.dim() == 2 else tuple(ints.shape)
+    ints = ints.contiguous()
+    words = torch.empty(e * k * n * bits // 32, dtype=torch.int32, device=ints.device)
+    lib = _lib.load()
+    _lib.check(lib.moe_pack_quantw(_ctx(ints.device), ints.data_ptr(), e, k, n, bits,
+                                   words.data_ptr()))
+    return QuantW(words, (e * k, n))
+
+
 def dispatch(route, num_experts: int):
     """The dispatch permutation the layer builds for `route` (diagnostic):
     (perm int32 [T·k], offsets int32 [E + 1])."""

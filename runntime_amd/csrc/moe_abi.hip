@@ -320,6 +320,18 @@ extern "C" int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int 
   return after_launch("dispatch");
 }
 
+extern "C" int moe_pack_quantw(moe_ctx *ctx, const int8_t *ints, int E, int k, int n, int bits,
+                               uint32_t *words) {
+  int rc = check_ctx(ctx, "packQuantW");
+  if (rc) return rc;
+  REQUIRE(bits == 8 || bits == 4, "packQuantW: bits must be 8 or 4");
+  REQUIRE(E >= 1 && k >= 4 && n >= 4 && k % 4 == 0 && n % 4 == 0,
+          "packQuantW: E >= 1 and k, n positive multiples of 4 required");
+  REQUIRE(ints && words, "packQuantW: NULL tensor");
+  if ((rc = launch_pack_quantw(ints, E, k, n, bits, words, ctx->stream))) return rc;
+  return after_launch("packQuantW");
+}
+
 extern "C" int moe_up(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *route,
                       const moe_expert_weight *glu, const moe_expert_weight *lin, int T, int K,
                       int N, int E, int k, int bits, int group_size, float *act) {

@@ -177,6 +177,8 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
 // replays it correctly).
 int launch_zero(float *p, size_t n, hipStream_t s);
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s] per call.
+int launch_pack_quantw(const int8_t *ints, int E, int k, int n, int bits, uint32_t *words,
+                       hipStream_t s);
 int launch_combine(const float *y, int64_t y_cs, const float *route, int64_t route_cs,
                    const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
                    int64_t out_cs, int calls, hipStream_t s);

@@ -160,3 +160,10 @@ def test_runntime_error_codes():
     assert not rt.is_runntime_error(ValueError("x"))
     with pytest.raises(ValueError):
         rt.RunntimeError("NOPE", "x")
+
+
+def test_pack_quant_w_device_rejects_host_or_wrong_dtype():
+    with pytest.raises(ValueError, match="packQuantW: ints must be a device int8"):
+        rt.pack_quant_w_device(torch.zeros((2, 8, 8), dtype=torch.int8))
+    with pytest.raises(ValueError, match="packQuantW"):
+        rt.pack_quant_w_device(torch.zeros((2, 8, 8), dtype=torch.int32))

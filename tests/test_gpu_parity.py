@@ -399,3 +399,17 @@ def test_graph_replay_matches_eager():
             torch.cuda.synchronize()
             assert torch.equal(route, want_route), f"replay {i}: route"
             assert torch.equal(out, want_out), f"replay {i}: out"
+
+
+# -------------------------------------------------------------- quantW pack
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("E,k,n", [(1, 4, 4), (3, 8, 12), (5, 64, 36), (2, 640, 640)])
+def test_pack_quant_w_device_matches_packquantw(bits, E, k, n):
+    say(f"pack int{bits} E={E} k={k} n={n}")
+    lo, hi = (-8, 8) if bits == 4 else (-128, 128)
+    ints = np.random.default_rng(E * 1000 + k + n).integers(lo, hi, size=(E, n, k), dtype=np.int8)
+    got = host(rt.pack_quant_w_device(gpu(ints), bits).words).view(np.uint32)
+    want = np.concatenate([ref.pack_nk(ints[e], k, n, bits) for e in range(E)])
+    np.testing.assert_array_equal(got, want)
