@@ -7,17 +7,29 @@
 //
 // Work: for every active expert e (rows grouped by the dispatch), C_e =
 // A_e · W_e with A_e the expert's gathered input rows (x for up, act for
-// down) and W_e its int8 weights. Up computes glu and lin for the same
-// outputs in one tile (64 glu + 64 lin columns) and applies the SwiGLU in the
-// epilogue; down adds the bias.
+// down) and W_e its int8 weights. Up computes glu and lin for the same 128
+// outputs in one tile (128 glu + 128 lin columns) and applies the SwiGLU in
+// the epilogue; down adds the bias.
 //
-// Tiles: 128 rows × 128 columns × 64-wide K steps, 4 wavefronts in a 2×2
-// grid, each with 2×2 v_mfma_f32_32x32x16_f16 tiles (64 × 64). Per K step the
-// block loads the int8 weight tiles (8 KB) and the gathered A rows into
-// registers one step ahead, then converts and stores them to LDS: weights
-// dequantized to f16 (exact: |q| ≤ 127), A as f16, or for f32 input as f16
-// hi + lo planes (two MFMAs; ~2^-22 relative). Scales (one per column and K
-// group) and biases run in the epilogue.
+// Tiles: 128 rows × 256 weight columns per block, 4 wavefronts side by side,
+// each owning all 128 rows × 64 columns (4 × 2 v_mfma_f32_32x32x16_f16
+// tiles, 128 accumulators, two wavefronts per SIMD): a weight fragment is
+// read and converted by exactly one wavefront. Reading the LDS fragments is
+// what bounds this kernel (measured: without those reads the same kernel
+// runs 30% faster; without the int8 conversion, 1%). Per K step the block's
+// global loads for the next step are issued first, the MFMAs run from one
+// LDS buffer, then the loaded data goes to the other buffer: one barrier
+// per step.
+//  - Weights stay int8 in LDS ([column][k] bytes, row pitch BK + 8: the
+//    8-byte fragment reads of 32 columns hit 64 distinct banks), stored
+//    with the sign bit flipped (q + 128 as a byte), and become f16 after the
+//    read (exact: |q| ≤ 127).
+//  - A is f16 in LDS ([row][k], pitch BK + 8 halves); f32 input is split
+//    into f16 hi + lo planes (two MFMAs per tile; ~2^-22 relative), with
+//    BK 32 instead of 64 so that a step holds the same MFMA work and two
+//    blocks still fit a CU's LDS.
+// Scales (one per column: the GEMM path runs with groupSize = K) and biases
+// apply in the epilogue.
 //
 // Order of tiles: expert, then N-tile, then M-tile, so the M-tiles of one
 // (expert, N-tile) — which share its weights — run back to back; blocks are
@@ -29,14 +41,17 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native vectors for the staging registers: HIP's uint4 struct is copied
+// through private memory when moved whole.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 16 bytes at an 8-byte aligned LDS address (weight rows have pitch BK + 8).
+typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
 
 constexpr int WAVE = 64;
-constexpr int BM = GEMM_TILE_M;  // 128
-constexpr int BN = 128;
-constexpr int BK = 64;
-constexpr int LDK = BK + 8;  // LDS row stride (halves): +16 B shifts rows 4 banks
+constexpr int BM = GEMM_TILE_M;  // 128 rows
+constexpr int BNW = 256;         // weight columns per block (up: 128 glu + 128 lin)
 
 struct GemmArgs {
   const void *a;
@@ -47,7 +62,7 @@ struct GemmArgs {
   const uint32_t *w1;  // lin (up)
   const float *s1;
   const float *b1;
-  int K, N, E, g;      // N: output columns (up: I, per projection)
+  int K, N, E;         // N: output columns (up: I, per projection)
   float *out;
   const int32_t *perm;
   const int32_t *active;  // [E][4] {e, first row, rows, first M-tile}
@@ -62,40 +77,37 @@ __device__ __forceinline__ float swiglu(float glu, float lin) {
   return (g / (1.0f + expf(-1.702f * g))) * (l + 1.0f);
 }
 
-// Two quantW column words (4 rows each, consecutive in K) → 8 f16 in K
-// order. Byte b becomes f16(1024 + (b ^ 0x80)), minus 1152 gives b.
-__device__ __forceinline__ half8 cvt_i8x8(uint32_t w0, uint32_t w1) {
+// 8 offset bytes u = q + 128 (k order, little-endian in two words) → 8 f16
+// q. Placing u under the exponent byte 0x64 gives the f16 1024 + u; minus
+// 1152 leaves q exactly.
+__device__ __forceinline__ uint32_t u8x2_to_h2(uint32_t x, uint32_t sel) {
   const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-  uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
-  half2v h0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - bias;
-  half2v h1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - bias;
-  half2v h2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - bias;
-  half2v h3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - bias;
-  half8 r;
-  r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-  r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-  return r;
+  return __builtin_bit_cast(
+      uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, sel)) - bias);
+}
+__device__ __forceinline__ half8 cvt_u8x8(uint32_t x0, uint32_t x1) {
+  const u32x4 r = {u8x2_to_h2(x0, 0x04010400u), u8x2_to_h2(x0, 0x04030402u),
+                   u8x2_to_h2(x1, 0x04010400u), u8x2_to_h2(x1, 0x04030402u)};
+  return __builtin_bit_cast(half8, r);
 }
 
-// Global loads of one K step: this thread's weight bytes and A elements.
-template <typename AT>
-struct Prefetch {
-  uint4 w[2];                                   // 32 B: two quantW tiles of one unit
-  uint4 a[sizeof(AT) == 4 ? 8 : 4];             // 32 consecutive k of one A row
-};
-
 template <int MODE, typename AT>
-__global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_expert_gemm(GemmArgs p) {
   constexpr bool SPLIT = sizeof(AT) == 4;
   constexpr int PLANES = SPLIT ? 2 : 1;
-  __shared__ __align__(16) _Float16 As[PLANES][BM * LDK];
-  __shared__ __align__(16) _Float16 Bs[BN * LDK];
+  constexpr int BK = SPLIT ? 32 : 64;
+  constexpr int LDA = BK + 8;   // halves
+  constexpr int LDW = BK + 8;   // bytes
+  constexpr int KT = BK / 16;   // quantW tiles (4 k each) per thread per step
+  __shared__ __align__(16) _Float16 As[2][PLANES][BM * LDA];
+  __shared__ __align__(16) uint8_t Ws[2][BNW * LDW];
 
   // ---- which tile: XCD-contiguous block order (gridDim.x is a multiple of
   // 8), then expert / N / M.
   const int nblk = gridDim.x;
   const int b = blockIdx.x;
-  const int per_xcd = (nblk + 7) / 8;
+  const int per_xcd = nblk / 8;
   const int L = (b % 8) * per_xcd + b / 8;
   const int total_tiles = p.meta[META_TILES];
   if (L >= total_tiles * p.nt) return;
@@ -118,51 +130,57 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
   const int wave = tid / WAVE;
-  const int wm = wave >> 1, wn = wave & 1;
   const int N4 = p.N / 4, K4 = p.K / 4;
   const int ksteps = p.K / BK;
 
   // ---- this thread's share of the staging
-  // Weights: unit ut (of the tile's 32), tiles 2·tp, 2·tp + 1 of the K step.
-  const int ut = tid >> 3, tp = tid & 7;
-  const uint32_t *wsrc;
-  int ucol;  // first of the unit's 4 columns in the tile's B (0..127)
+  // Weights: block unit bu (of 64, 4 columns each), tiles KT·q .. KT·q + KT − 1
+  // of the step. Up: units 0..31 are glu, 32..63 lin, of the same outputs.
+  const int bu = tid >> 2, q = tid & 3;
+  int u;
+  const uint32_t *wbase;
   if (MODE == MODE_UP) {
-    const bool second = ut >= 16;  // lin units follow the glu units
-    const int u = ntile * 16 + (ut & 15);
-    wsrc = (second ? p.w1 : p.w0) + ((int64_t)e * N4 + u) * K4 * 4;
-    ucol = (second ? 64 : 0) + (ut & 15) * 4;
+    u = ntile * 32 + (bu & 31);
+    wbase = bu < 32 ? p.w0 : p.w1;
   } else {
-    const int u = ntile * 32 + ut;
-    wsrc = p.w0 + ((int64_t)e * N4 + u) * K4 * 4;
-    ucol = ut * 4;
+    u = ntile * 64 + bu;
+    wbase = p.w0;
   }
-  // A: row ar of the tile, 32 consecutive k from ak.
-  const int ar = tid >> 1, ak = (tid & 1) * 32;
-  const bool arow_ok = ar < rows;
-  const int64_t asrc_row = arow_ok ? p.perm[row0 + m0 + ar] / p.a_row_div : 0;
-  const AT *asrc = (const AT *)p.a + asrc_row * p.K + ak;
+  // Columns past N read unit 0 and rows past the tile's read its last row:
+  // MFMA rows and columns are independent, and the epilogue writes neither.
+  const u32x4 *wsrc = (const u32x4 *)(wbase + ((int64_t)e * N4 + (u < N4 ? u : 0)) * K4 * 4) + KT * q;
+  // A: row ar of the tile, BK/2 consecutive k from ak (64 bytes either way).
+  const int ar = tid >> 1, ak = (tid & 1) * (BK / 2);
+  const int64_t asrc_row = p.perm[row0 + m0 + min(ar, rows - 1)] / p.a_row_div;
+  const u32x4 *asrc = (const u32x4 *)((const AT *)p.a + asrc_row * p.K + ak);
 
-  auto load = [&](int ks, Prefetch<AT> &f) {
-    const uint4 *wp = (const uint4 *)wsrc + ks * (BK / 4) + 2 * tp;
-    f.w[0] = wp[0];
-    f.w[1] = wp[1];
-    const uint4 *ap = (const uint4 *)(asrc + ks * BK);
+  // Staging registers of one K step.
+  u32x4 wreg[KT], areg[4];
+  auto load = [&](int ks) {
 #pragma unroll
-    for (int i = 0; i < (SPLIT ? 8 : 4); i++) f.a[i] = arow_ok ? ap[i] : uint4{0, 0, 0, 0};
+    for (int i = 0; i < KT; i++) wreg[i] = wsrc[ks * (BK / 4) + i];
+#pragma unroll
+    for (int i = 0; i < 4; i++) areg[i] = asrc[ks * (BK * (int)sizeof(AT) / 16) + i];
   };
-  auto store = [&](const Prefetch<AT> &f) {
-    // weights: 4 columns × 8 k each, k contiguous per column
-    const uint32_t w0[4] = {f.w[0].x, f.w[0].y, f.w[0].z, f.w[0].w};
-    const uint32_t w1[4] = {f.w[1].x, f.w[1].y, f.w[1].z, f.w[1].w};
+  auto store = [&](int buf) {
+    // Tile i, word c = column c, rows 4(KT·q + i) .. +3 (one byte each).
+    constexpr uint32_t FLIP = 0x80808080u;
+    auto put = [&](int c, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+      uint8_t *dst = &Ws[buf][(bu * 4 + c) * LDW + q * KT * 4];
+      if constexpr (KT == 4)
+        *(u32x4_a8 *)dst = u32x4_a8{w0, w1, w2, w3} ^ FLIP;
+      else
+        *(u32x2 *)dst = u32x2{w0, w1} ^ FLIP;
+    };
+    const u32x4 t0 = wreg[0], t1 = wreg[1], t2 = wreg[KT == 4 ? 2 : 0], t3 = wreg[KT == 4 ? 3 : 1];
+    put(0, t0.x, t1.x, t2.x, t3.x);
+    put(1, t0.y, t1.y, t2.y, t3.y);
+    put(2, t0.z, t1.z, t2.z, t3.z);
+    put(3, t0.w, t1.w, t2.w, t3.w);
+    if constexpr (SPLIT) {
+      const float *v = (const float *)areg;  // 16 k
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      *(half8 *)&Bs[(ucol + c) * LDK + tp * 8] = cvt_i8x8(w0[c], w1[c]);
-    // A
-    if (SPLIT) {
-      const float *v = (const float *)f.a;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < 2; j++) {
         half8 h, l;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -171,18 +189,21 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs p) {
           h[i] = xh;
           l[i] = (_Float16)(x - (float)xh);
         }
-        *(half8 *)&As[0][ar * LDK + ak + 8 * j] = h;
-        *(half8 *)&As[PLANES - 1][ar * LDK + ak + 8 * j] = l;
+        *(half8 *)&As[buf][0][ar * LDA + ak + 8 * j] = h;
+        *(half8 *)&As[buf][PLANES - 1][ar * LDA + ak + 8 * j] = l;
       }
     } else {
-#pragma unroll
-      for (int j = 0; j < 4; j++) *(uint4 *)&As[0][ar * LDK + ak + 8 * j] = f.a[j];
+      u32x4 *dst = (u32x4 *)&As[buf][0][ar * LDA + ak];
+      dst[0] = areg[0];
+      dst[1] = areg[1];
+      dst[2] = areg[2];
+      dst[3] = areg[3];
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -191,66 +212,81 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs p) {
   // MFMA operands: lane L reads row (or column) L%32, k 8·(L/32) .. +7 of a
   // 16-wide K slice.
   const int fr = lane & 31, fk = (lane >> 5) * 8;
-  // B column tiles of this wavefront: up → glu cols 32·wn.. and the lin cols
-  // at +64 (so each wavefront holds matching glu/lin sums); down → 64·wn, +32.
-  const int bc0 = MODE == MODE_UP ? 32 * wn : 64 * wn;
-  const int bc1 = MODE == MODE_UP ? 64 + 32 * wn : 64 * wn + 32;
+  // Weight columns of this wavefront's tiles: up → glu 32·wave (j = 0) and
+  // the matching lin columns at +128 (j = 1); down → 64·wave + 32j.
+  const int wcol[2] = {MODE == MODE_UP ? 32 * wave : 64 * wave,
+                       MODE == MODE_UP ? 128 + 32 * wave : 64 * wave + 32};
 
-  Prefetch<AT> f;
-  load(0, f);
-  for (int ks = 0; ks < ksteps; ks++) {
-    __syncthreads();  // the previous step's LDS reads are done
-    store(f);
-    __syncthreads();
-    if (ks + 1 < ksteps) load(ks + 1, f);
+  auto compute = [&](int cur) {
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       half8 bf[2];
-      bf[0] = *(const half8 *)&Bs[(bc0 + fr) * LDK + kk + fk];
-      bf[1] = *(const half8 *)&Bs[(bc1 + fr) * LDK + kk + fk];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const u32x2 raw = *(const u32x2 *)&Ws[cur][(wcol[j] + fr) * LDW + kk + fk];
+        bf[j] = cvt_u8x8(raw.x, raw.y);
+      }
 #pragma unroll
       for (int pl = 0; pl < PLANES; pl++) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-          const half8 af = *(const half8 *)&As[pl][(wm * 64 + i * 32 + fr) * LDK + kk + fk];
+        for (int i = 0; i < 4; i++) {
+          const half8 af = *(const half8 *)&As[cur][pl][(i * 32 + fr) * LDA + kk + fk];
 #pragma unroll
           for (int j = 0; j < 2; j++)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
         }
       }
     }
+  };
+
+  // Step s computes LDS buffer s & 1 while step s + 1 loads into registers;
+  // then step s + 1 goes to the other buffer. The last step re-reads itself (unconditional: a branch would keep the
+  // staging registers in memory).
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int ks = 0; ks < ksteps; ks++) {
+    const int cur = ks & 1;
+    load(min(ks + 1, ksteps - 1));
+    compute(cur);
+    // Keep the staging work (which waits for the loads above) after the
+    // MFMAs: hoisted into them it would stall each step on the loads.
+    __builtin_amdgcn_sched_barrier(0);
+    store(cur ^ 1);
+    __syncthreads();
   }
 
-  // ---- epilogue. acc[i][j][r]: row wm·64 + 32i + 8(r/4) + 4(L/32) + r%4,
-  // column (of tile j) L%32.
-  const int kg = p.K / p.g;  // the GEMM path runs with one scale group
-  (void)kg;
+  // ---- epilogue. acc[i][j][r]: row 32i + 8(r/4) + 4(L/32) + r%4, column
+  // L%32 of tile j.
   if (MODE == MODE_UP) {
-    const int col = ntile * 64 + 32 * wn + fr;  // output column (glu index = lin index)
-    const float sg = p.s0[(int64_t)e * p.N + col], sl = p.s1[(int64_t)e * p.N + col];
-    const float bg = p.b0 ? p.b0[(int64_t)e * p.N + col] : 0.f;
-    const float bl = p.b1 ? p.b1[(int64_t)e * p.N + col] : 0.f;
+    const int col = ntile * 128 + 32 * wave + fr;  // glu index = lin index
+    if (col < p.N) {
+      const float sg = p.s0[(int64_t)e * p.N + col], sl = p.s1[(int64_t)e * p.N + col];
+      const float bg = p.b0 ? p.b0[(int64_t)e * p.N + col] : 0.f;
+      const float bl = p.b1 ? p.b1[(int64_t)e * p.N + col] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-        if (row < rows) {
-          const int64_t asg = p.perm[row0 + m0 + row];
-          p.out[asg * p.N + col] = swiglu(acc[i][0][r] * sg + bg, acc[i][1][r] * sl + bl);
+        for (int r = 0; r < 16; r++) {
+          const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          if (row < rows) {
+            const int64_t asg = p.perm[row0 + m0 + row];
+            p.out[asg * p.N + col] = swiglu(acc[i][0][r] * sg + bg, acc[i][1][r] * sl + bl);
+          }
         }
-      }
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int col = ntile * BN + (j == 0 ? bc0 : bc1) + fr;
+      const int col = ntile * BNW + wcol[j] + fr;
+      if (col >= p.N) continue;
       const float sc = p.s0[(int64_t)e * p.N + col];
       const float bb = p.b0 ? p.b0[(int64_t)e * p.N + col] : 0.f;
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int row = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
           if (row < rows) {
             const int64_t asg = p.perm[row0 + m0 + row];
             p.out[asg * p.N + col] = acc[i][j][r] * sc + bb;
@@ -263,9 +299,9 @@ __global__ __launch_bounds__(256) void k_expert_gemm(GemmArgs p) {
 }  // namespace
 
 bool gemm_eligible(const ExpertArgs &ea) {
-  // One scale group per column, K in whole steps, N in whole tiles.
-  const int tile_cols = ea.mode == MODE_UP ? 64 : BN;
-  return ea.bits == 8 && ea.g == ea.K && ea.K % BK == 0 && ea.N % tile_cols == 0;
+  // One scale group per column, K in whole steps.
+  const int bk = ea.a_dtype == MOE_F16 ? 64 : 32;
+  return ea.bits == 8 && ea.g == ea.K && ea.K % bk == 0 && ea.N % 4 == 0;
 }
 
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
@@ -283,12 +319,12 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   p.K = ea.K;
   p.N = ea.N;
   p.E = ea.E;
-  p.g = ea.g;
   p.out = ea.out;
   p.perm = db.perm;
   p.active = db.active;
   p.meta = db.meta;
-  p.nt = ea.mode == MODE_UP ? ea.N / 64 : ea.N / BN;
+  const int cols = ea.mode == MODE_UP ? BNW / 2 : BNW;  // output columns per tile
+  p.nt = (ea.N + cols - 1) / cols;
   // Upper bound of M-tiles over all experts: each active expert adds at most
   // one partial tile.
   const int a_tiles = (ea.A + BM - 1) / BM + (ea.E < ea.A ? ea.E : ea.A);
