@@ -57,10 +57,14 @@ struct ExpertKArgs {
 };
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
-  // activations.ts:127-133: g = min(glu, 7), l = clamp(lin, ±7).
-  float g = fminf(glu, 7.0f);
-  float l = fminf(fmaxf(lin, -7.0f), 7.0f);
-  return (g / (1.0f + expf(-1.702f * g))) * (l + 1.0f);
+  // activations.ts:127-133: g = min(glu, 7), l = clamp(lin, ±7),
+  // g / (1 + exp(−1.702·g)) · (l + 1). exp via the hardware 2^x and the
+  // quotient via the hardware reciprocal (each within 1 ulp): the precise
+  // library forms cost more VALU than the GEMM epilogue can hide.
+  const float g = fminf(glu, 7.0f);
+  const float l = fminf(fmaxf(lin, -7.0f), 7.0f);
+  const float e = __builtin_amdgcn_exp2f(g * (-1.702f * 1.4426950408889634f));
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * (l + 1.0f);
 }
 
 // Two quantW column words (rows r0..r3 of tile k4 and of tile k4+1) → 8 f16

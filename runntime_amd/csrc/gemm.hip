@@ -71,10 +71,14 @@ struct GemmArgs {
 };
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
-  // activations.ts:127-133: g = min(glu, 7), l = clamp(lin, ±7).
-  float g = fminf(glu, 7.0f);
-  float l = fminf(fmaxf(lin, -7.0f), 7.0f);
-  return (g / (1.0f + expf(-1.702f * g))) * (l + 1.0f);
+  // activations.ts:127-133: g = min(glu, 7), l = clamp(lin, ±7),
+  // g / (1 + exp(−1.702·g)) · (l + 1). exp via the hardware 2^x and the
+  // quotient via the hardware reciprocal (each within 1 ulp): the precise
+  // library forms cost more VALU than the GEMM epilogue can hide.
+  const float g = fminf(glu, 7.0f);
+  const float l = fminf(fmaxf(lin, -7.0f), 7.0f);
+  const float e = __builtin_amdgcn_exp2f(g * (-1.702f * 1.4426950408889634f));
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * (l + 1.0f);
 }
 
 // 8 offset bytes u = q + 128 (k order, little-endian in two words) → 8 f16
@@ -102,6 +106,7 @@ void k_expert_gemm(GemmArgs p) {
   constexpr int KT = BK / 16;   // quantW tiles (4 k each) per thread per step
   __shared__ __align__(16) _Float16 As[2][PLANES][BM * LDA];
   __shared__ __align__(16) uint8_t Ws[2][BNW * LDW];
+  __shared__ int32_t rowmap[BM];  // assignment of each tile row (for the epilogue)
 
   // ---- which tile: XCD-contiguous block order (gridDim.x is a multiple of
   // 8), then expert / N / M.
@@ -151,7 +156,9 @@ void k_expert_gemm(GemmArgs p) {
   const u32x4 *wsrc = (const u32x4 *)(wbase + ((int64_t)e * N4 + (u < N4 ? u : 0)) * K4 * 4) + KT * q;
   // A: row ar of the tile, BK/2 consecutive k from ak (64 bytes either way).
   const int ar = tid >> 1, ak = (tid & 1) * (BK / 2);
-  const int64_t asrc_row = p.perm[row0 + m0 + min(ar, rows - 1)] / p.a_row_div;
+  const int32_t asg_ar = p.perm[row0 + m0 + min(ar, rows - 1)];
+  if ((tid & 1) == 0) rowmap[ar] = asg_ar;  // read after the loop's barriers
+  const int64_t asrc_row = asg_ar / p.a_row_div;
   const u32x4 *asrc = (const u32x4 *)((const AT *)p.a + asrc_row * p.K + ak);
 
   // Staging registers of one K step.
@@ -270,7 +277,7 @@ void k_expert_gemm(GemmArgs p) {
         for (int r = 0; r < 16; r++) {
           const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
           if (row < rows) {
-            const int64_t asg = p.perm[row0 + m0 + row];
+            const int64_t asg = rowmap[row];
             p.out[asg * p.N + col] = swiglu(acc[i][0][r] * sg + bg, acc[i][1][r] * sl + bl);
           }
         }
@@ -288,7 +295,7 @@ void k_expert_gemm(GemmArgs p) {
         for (int r = 0; r < 16; r++) {
           const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
           if (row < rows) {
-            const int64_t asg = p.perm[row0 + m0 + row];
+            const int64_t asg = rowmap[row];
             p.out[asg * p.N + col] = acc[i][j][r] * sc + bb;
           }
         }
