@@ -7,63 +7,88 @@
 //
 // Work: for every active expert e (rows grouped by the dispatch), C_e =
 // A_e · W_e with A_e the expert's gathered input rows (x for up, act for
-// down) and W_e its int8 weights. Up computes glu and lin for the same 128
-// outputs in one tile (128 glu + 128 lin columns) and applies the SwiGLU in
-// the epilogue; down adds the bias.
+// down) and W_e its int8 weights. Up computes glu and lin for the same
+// outputs in one tile and applies the SwiGLU in the epilogue; down adds the
+// bias.
 //
-// Tiles: 128 rows × 256 weight columns per block, 4 wavefronts side by side,
-// each owning all 128 rows × 64 columns (4 × 2 v_mfma_f32_32x32x16_f16
-// tiles, 128 accumulators, two wavefronts per SIMD): a weight fragment is
-// read and converted by exactly one wavefront. Reading the LDS fragments is
-// what bounds this kernel (measured: without those reads the same kernel
-// runs 30% faster; without the int8 conversion, 1%). Per K step the block's
-// global loads for the next step are issued first, the MFMAs run from one
-// LDS buffer, then the loaded data goes to the other buffer: one barrier
-// per step.
-//  - Weights stay int8 in LDS ([column][k] bytes, row pitch BK + 8: the
-//    8-byte fragment reads of 32 columns hit 64 distinct banks), stored
-//    with the sign bit flipped (q + 128 as a byte), and become f16 after the
-//    read (exact: |q| ≤ 127).
-//  - A is f16 in LDS ([row][k], pitch BK + 8 halves); f32 input is split
-//    into f16 hi + lo planes (two MFMAs per tile; ~2^-22 relative), with
-//    BK 32 instead of 64 so that a step holds the same MFMA work and two
-//    blocks still fit a CU's LDS.
-// Scales (one per column: the GEMM path runs with groupSize = K) and biases
-// apply in the epilogue.
+// Tiles: 128 rows × 128 weight units (512 columns) per block, eight
+// wavefronts as 2 (rows) × 4 (units), each owning 64 rows × 32 units: 2 × 4
+// v_mfma_f32_32x32x16_f16 tiles (128 accumulators, two wavefronts per
+// SIMD). The block's units come from two sources of 64 units each: up takes
+// the same 64 units (256 outputs) of glu and of lin, down takes 128
+// consecutive units of its one weight (512 outputs). An up wavefront's 32
+// units are 16 of glu (lanes 0-15 of a half) and the same 16 of lin (lanes
+// 16-31), so the SwiGLU pairs lanes 16 apart. Each converted weight
+// fragment feeds two MFMAs: the int8 → f16 conversion (VALU) is what bounds
+// a wavefront tile one MFMA tall. A 128 × 512 tile per CU
+// is what the register file holds; its operands (16 KB of f16 A and 32 KB of
+// int8 weights per 64 k) come through L2, whose bandwidth and latency bound
+// this kernel together with the MFMAs.
+//
+// Weights go to LDS as the quantW words are: 16-byte tiles of 4 columns × 4
+// k, [column][k] bytes, so dword c of a tile is column c's four k values.
+// A lane of the MFMA B operand owns one unit (L % 32) and, per 16-k slice,
+// two tiles (32 bytes): that is columns c = 0..3 of its unit with 8 k each,
+// the B operands of four MFMAs whose 32 columns are "column c of units
+// 0..31". The k order inside a 32-k step is a fixed permutation (lane half
+// h, slice kk holds k = 16h + 8kk .. +7) that A follows too, so the sum is
+// unchanged. int8 → f16 is exact (|q| ≤ 127).
+//
+// Loads go straight from global memory to LDS (buffer_load … lds): a ring of
+// STAGES steps, STAGES − 1 of them in flight while one is computed; no
+// staging registers and no LDS stores. Each step: wait for this wavefront's
+// loads of the step, barrier (all wavefronts' loads landed, and the previous
+// step's LDS reads are done), issue the loads of the step STAGES − 1 ahead
+// into the slot just freed, compute. The waits are explicit vmcnt counts:
+// the compiler does not track loads that write LDS.
+//
+// LDS positions are XOR-swizzled so that the 16-byte fragment reads of any
+// 8 or 16 consecutive lanes hit distinct banks. Rows of 128 bytes (a
+// weight slot's 8 tiles, an f32 A row): chunk c of row r at
+// r·128 + ((c ^ sw8(r))·16), sw8(r) = (r ^ (r >> 3)) & 7. Rows of 64 bytes
+// (an f16 A row): r·64 + ((c ^ sw4(r))·16), sw4(r) = ((r >> 1) ^ (r >> 3)) & 3.
+// f32 A is split into f16 hi + lo after the read (two MFMAs per product;
+// ~2^-22 relative).
 //
 // Order of tiles: expert, then N-tile, then M-tile, so the M-tiles of one
 // (expert, N-tile) — which share its weights — run back to back; blocks are
-// then dealt to the 8 XCDs in contiguous ranges (block b runs on XCD b mod 8),
+// dealt to the 8 XCDs in contiguous ranges (block b runs on XCD b mod 8),
 // so those neighbours share one L2.
 #include "moe_internal.h"
+
+#include <type_traits>
 
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-// Native vectors for the staging registers: HIP's uint4 struct is copied
-// through private memory when moved whole.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-// 16 bytes at an 8-byte aligned LDS address (weight rows have pitch BK + 8).
-typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
 constexpr int BM = GEMM_TILE_M;  // 128 rows
-constexpr int BNW = 256;         // weight columns per block (up: 128 glu + 128 lin)
+constexpr int BK = 32;           // k per step
+constexpr int TPS = BK / 4;      // quantW tiles per unit per step
+constexpr int SLOTS = 128;       // weight units per block (2 sources × 64)
+constexpr int W_BYTES = SLOTS * TPS * 16;  // weights of one step: 16 KB
+// Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format).
+constexpr int BUF_DWORD3 = 0x00020000;
 
 struct GemmArgs {
   const void *a;
+  int a_bytes;  // size of a (bounds of its buffer loads)
   int a_row_div;
   const uint32_t *w0;  // glu (up) or down
   const float *s0;
   const float *b0;
-  const uint32_t *w1;  // lin (up)
+  const uint32_t *w1;  // lin (up); down: w0 again
   const float *s1;
   const float *b1;
   int K, N, E;         // N: output columns (up: I, per projection)
   float *out;
+  int out_bytes;  // size of out (bounds of its buffer stores)
   const int32_t *perm;
   const int32_t *active;  // [E][4] {e, first row, rows, first M-tile}
   const int32_t *meta;
@@ -81,32 +106,53 @@ __device__ __forceinline__ float swiglu(float glu, float lin) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * (l + 1.0f);
 }
 
-// 8 offset bytes u = q + 128 (k order, little-endian in two words) → 8 f16
-// q. Placing u under the exponent byte 0x64 gives the f16 1024 + u; minus
-// 1152 leaves q exactly.
+// 8 int8 q (k order, little-endian in two words) → 8 f16 q. Flipping the
+// sign bit gives u = q + 128; placing u under the exponent byte 0x64 gives
+// the f16 1024 + u; minus 1152 leaves q exactly.
 __device__ __forceinline__ uint32_t u8x2_to_h2(uint32_t x, uint32_t sel) {
   const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
   return __builtin_bit_cast(
       uint32_t, __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x, sel)) - bias);
 }
-__device__ __forceinline__ half8 cvt_u8x8(uint32_t x0, uint32_t x1) {
+__device__ __forceinline__ half8 cvt_i8x8(uint32_t x0, uint32_t x1) {
+  x0 ^= 0x80808080u;
+  x1 ^= 0x80808080u;
   const u32x4 r = {u8x2_to_h2(x0, 0x04010400u), u8x2_to_h2(x0, 0x04030402u),
                    u8x2_to_h2(x1, 0x04010400u), u8x2_to_h2(x1, 0x04030402u)};
   return __builtin_bit_cast(half8, r);
 }
 
+__device__ __forceinline__ int sw8(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int sw4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// One buffer_load_dwordx4 … lds: 16 bytes per lane from rsrc at voff + soff
+// into LDS at lds_addr + 16·lane. Written as asm so that the compiler, which
+// does not track these loads, adds no waits for them; the loop's explicit
+// vmcnt waits order them. (The compiler's own waits for other vector loads
+// only count its own loads and so can only wait longer with these in
+// flight.) M0 holds the LDS address; nothing else in this kernel uses M0.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, int soff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr) : "memory");
+}
+__device__ __forceinline__ i32x4 buffer_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, BUF_DWORD3};
+}
+
+// s_waitcnt with vmcnt = n (< 16) and no wait on the other counters.
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
+
 template <int MODE, typename AT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_expert_gemm(GemmArgs p) {
   constexpr bool SPLIT = sizeof(AT) == 4;
-  constexpr int PLANES = SPLIT ? 2 : 1;
-  constexpr int BK = SPLIT ? 32 : 64;
-  constexpr int LDA = BK + 8;   // halves
-  constexpr int LDW = BK + 8;   // bytes
-  constexpr int KT = BK / 16;   // quantW tiles (4 k each) per thread per step
-  __shared__ __align__(16) _Float16 As[2][PLANES][BM * LDA];
-  __shared__ __align__(16) uint8_t Ws[2][BNW * LDW];
-  __shared__ int32_t rowmap[BM];  // assignment of each tile row (for the epilogue)
+  constexpr int A_BYTES = BM * BK * (int)sizeof(AT);  // 8 or 16 KB
+  constexpr int STAGE = W_BYTES + A_BYTES;
+  constexpr int STAGES = SPLIT ? 4 : 6;               // 128 or 144 KB
+  constexpr int LOADS = SPLIT ? 4 : 3;                // per thread per step
+  __shared__ __align__(16) uint8_t lds[STAGES * STAGE];
+  __shared__ int32_t rowmap[BM];  // assignment of each tile row
 
   // ---- which tile: XCD-contiguous block order (gridDim.x is a multiple of
   // 8), then expert / N / M.
@@ -134,172 +180,217 @@ void k_expert_gemm(GemmArgs p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
-  const int wave = tid / WAVE;
-  const int N4 = p.N / 4, K4 = p.K / 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform
+  const int wm = wave & 1, wn = wave >> 1;
+  const int N4 = p.N / 4;
   const int ksteps = p.K / BK;
+  // First unit of each source.
+  const int U0 = MODE == MODE_UP ? ntile * 64 : ntile * 128;
+  const int U1 = MODE == MODE_UP ? ntile * 64 : ntile * 128 + 64;
 
-  // ---- this thread's share of the staging
-  // Weights: block unit bu (of 64, 4 columns each), tiles KT·q .. KT·q + KT − 1
-  // of the step. Up: units 0..31 are glu, 32..63 lin, of the same outputs.
-  const int bu = tid >> 2, q = tid & 3;
-  int u;
-  const uint32_t *wbase;
-  if (MODE == MODE_UP) {
-    u = ntile * 32 + (bu & 31);
-    wbase = bu < 32 ? p.w0 : p.w1;
-  } else {
-    u = ntile * 64 + bu;
-    wbase = p.w0;
+  if (tid < BM) rowmap[tid] = p.perm[row0 + m0 + min(tid, rows - 1)];
+  __syncthreads();
+
+  // ---- this wavefront's loads of a step. Each load instruction fills 1 KB
+  // of LDS (lane l at +16·l), so lane l picks the global chunk that belongs
+  // at that position.
+  // Weights: instructions i = 0, 1 fill slots 16·wave + 8i .. +7 (wavefronts
+  // 0-3: source 0, 4-7: source 1); lane l: slot + (l >> 3), position l & 7
+  // holds tile (l & 7) ^ sw8(slot). A unit past N gets an offset past the
+  // expert's slab, which the buffer's range check turns into zeros.
+  // A: f16 → one instruction, rows 16·wave + (l >> 2), position l & 3 holds
+  //    8-half chunk (l & 3) ^ sw4(row); f32 → instructions i = 0, 1, rows
+  //    16·wave + 8i + (l >> 3), position l & 7 holds 4-float chunk
+  //    (l & 7) ^ sw8(row). Rows past the tile's read its last row: MFMA rows
+  //    are independent and the epilogue writes none of them.
+  const uint32_t slab = (uint32_t)p.K * (uint32_t)p.N;  // bytes of one expert
+  const i32x4 wr = buffer_rsrc((wave < 4 ? p.w0 : p.w1) + (int64_t)e * (slab / 4), slab);
+  const i32x4 ar = buffer_rsrc(p.a, (uint32_t)p.a_bytes);
+  // LDS byte address of the ring.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+  uint32_t woff[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int slot = 16 * wave + 8 * i + (lane >> 3);
+    const int u = (wave < 4 ? U0 : U1) + (slot & 63);
+    const int tile = (lane & 7) ^ sw8(slot);
+    woff[i] = u < N4 ? (uint32_t)u * (uint32_t)p.K * 4u + tile * 16u : 0x80000000u;
   }
-  // Columns past N read unit 0 and rows past the tile's read its last row:
-  // MFMA rows and columns are independent, and the epilogue writes neither.
-  const u32x4 *wsrc = (const u32x4 *)(wbase + ((int64_t)e * N4 + (u < N4 ? u : 0)) * K4 * 4) + KT * q;
-  // A: row ar of the tile, BK/2 consecutive k from ak (64 bytes either way).
-  const int ar = tid >> 1, ak = (tid & 1) * (BK / 2);
-  const int32_t asg_ar = p.perm[row0 + m0 + min(ar, rows - 1)];
-  if ((tid & 1) == 0) rowmap[ar] = asg_ar;  // read after the loop's barriers
-  const int64_t asrc_row = asg_ar / p.a_row_div;
-  const u32x4 *asrc = (const u32x4 *)((const AT *)p.a + asrc_row * p.K + ak);
-
-  // Staging registers of one K step.
-  u32x4 wreg[KT], areg[4];
-  auto load = [&](int ks) {
+  constexpr int AI = SPLIT ? 2 : 1;
+  uint32_t aoffg[AI];
 #pragma unroll
-    for (int i = 0; i < KT; i++) wreg[i] = wsrc[ks * (BK / 4) + i];
-#pragma unroll
-    for (int i = 0; i < 4; i++) areg[i] = asrc[ks * (BK * (int)sizeof(AT) / 16) + i];
-  };
-  auto store = [&](int buf) {
-    // Tile i, word c = column c, rows 4(KT·q + i) .. +3 (one byte each).
-    constexpr uint32_t FLIP = 0x80808080u;
-    auto put = [&](int c, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
-      uint8_t *dst = &Ws[buf][(bu * 4 + c) * LDW + q * KT * 4];
-      if constexpr (KT == 4)
-        *(u32x4_a8 *)dst = u32x4_a8{w0, w1, w2, w3} ^ FLIP;
-      else
-        *(u32x2 *)dst = u32x2{w0, w1} ^ FLIP;
-    };
-    const u32x4 t0 = wreg[0], t1 = wreg[1], t2 = wreg[KT == 4 ? 2 : 0], t3 = wreg[KT == 4 ? 3 : 1];
-    put(0, t0.x, t1.x, t2.x, t3.x);
-    put(1, t0.y, t1.y, t2.y, t3.y);
-    put(2, t0.z, t1.z, t2.z, t3.z);
-    put(3, t0.w, t1.w, t2.w, t3.w);
-    if constexpr (SPLIT) {
-      const float *v = (const float *)areg;  // 16 k
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        half8 h, l;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float x = v[8 * j + i];
-          const _Float16 xh = (_Float16)x;
-          h[i] = xh;
-          l[i] = (_Float16)(x - (float)xh);
-        }
-        *(half8 *)&As[buf][0][ar * LDA + ak + 8 * j] = h;
-        *(half8 *)&As[buf][PLANES - 1][ar * LDA + ak + 8 * j] = l;
-      }
+  for (int i = 0; i < AI; i++) {
+    if (SPLIT) {
+      const int r = 16 * wave + 8 * i + (lane >> 3);
+      const uint32_t srow = (uint32_t)(rowmap[r] / p.a_row_div);
+      aoffg[i] = srow * (uint32_t)p.K * 4u + ((lane & 7) ^ sw8(r)) * 16u;
     } else {
-      u32x4 *dst = (u32x4 *)&As[buf][0][ar * LDA + ak];
-      dst[0] = areg[0];
-      dst[1] = areg[1];
-      dst[2] = areg[2];
-      dst[3] = areg[3];
+      const int r = 16 * wave + (lane >> 2);
+      const uint32_t srow = (uint32_t)(rowmap[r] / p.a_row_div);
+      aoffg[i] = srow * (uint32_t)p.K * 2u + ((lane & 3) ^ sw4(r)) * 16u;
     }
+  }
+  auto issue = [&](int ks, int stage) {
+    const uint32_t st = lds0 + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < 2; i++) dma16(wr, woff[i], ks * (TPS * 16), st + (2 * wave + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < AI; i++)
+      dma16(ar, aoffg[i], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + i) * 1024);
   };
 
-  floatx16 acc[4][2];
+  floatx16 acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  // MFMA operands: lane L reads row (or column) L%32, k 8·(L/32) .. +7 of a
-  // 16-wide K slice.
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
-  // Weight columns of this wavefront's tiles: up → glu 32·wave (j = 0) and
-  // the matching lin columns at +128 (j = 1); down → 64·wave + 32j.
-  const int wcol[2] = {MODE == MODE_UP ? 32 * wave : 64 * wave,
-                       MODE == MODE_UP ? 128 + 32 * wave : 64 * wave + 32};
+  // Fragment positions. B: this lane's slot (up: glu unit 16·wn + (lm & 15)
+  // for lm < 16, the same lin unit for lm ≥ 16; down: slot 32·wn + lm),
+  // tiles 4h + 2kk (+1). A: rows 64·wm + 32i + lm, k 16h + 8kk .. +7.
+  const int lm = lane & 31, h = lane >> 5;
+  const int slot = MODE == MODE_UP ? (lm < 16 ? 0 : 64) + 16 * wn + (lm & 15) : 32 * wn + lm;
+  const int boff = slot * 128, bsw = sw8(slot);
+  int aoff[2], asw[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int arow = 64 * wm + 32 * i + lm;
+    aoff[i] = W_BYTES + arow * BK * (int)sizeof(AT);
+    asw[i] = SPLIT ? sw8(arow) : sw4(arow);
+  }
+  // First unit of this wavefront (both halves for up).
+  const int wu = MODE == MODE_UP ? U0 + 16 * wn : (wn < 2 ? U0 : U1) + 32 * (wn & 1);
+  // Waves whose units are all past N skip the MFMAs (uniform per wave).
+  const bool live = wu < N4;
 
-  auto compute = [&](int cur) {
+  auto compute = [&](int stage) {
+    const uint8_t *st = lds + stage * STAGE;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      half8 bf[2];
+    for (int kk = 0; kk < 2; kk++) {
+      half8 bf[4];
+      const int t0 = 4 * h + 2 * kk;
+      const u32x4 d0 = *(const u32x4 *)(st + boff + ((t0 ^ bsw) * 16));
+      const u32x4 d1 = *(const u32x4 *)(st + boff + (((t0 + 1) ^ bsw) * 16));
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const u32x2 raw = *(const u32x2 *)&Ws[cur][(wcol[j] + fr) * LDW + kk + fk];
-        bf[j] = cvt_u8x8(raw.x, raw.y);
-      }
+      for (int c = 0; c < 4; c++) bf[c] = cvt_i8x8(d0[c], d1[c]);
 #pragma unroll
-      for (int pl = 0; pl < PLANES; pl++) {
+      for (int i = 0; i < 2; i++) {
+        half8 af[SPLIT ? 2 : 1];
+        if constexpr (SPLIT) {
+          const floatx4 v0 = *(const floatx4 *)(st + aoff[i] + ((t0 ^ asw[i]) * 16));
+          const floatx4 v1 = *(const floatx4 *)(st + aoff[i] + (((t0 + 1) ^ asw[i]) * 16));
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const half8 af = *(const half8 *)&As[cur][pl][(i * 32 + fr) * LDA + kk + fk];
-#pragma unroll
-          for (int j = 0; j < 2; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 8; j++) {
+            const float x = j < 4 ? v0[j] : v1[j - 4];
+            const _Float16 xh = (_Float16)x;
+            af[0][j] = xh;
+            af[1][j] = (_Float16)(x - (float)xh);
+          }
+        } else {
+          af[0] = *(const half8 *)(st + aoff[i] + (((2 * h + kk) ^ asw[i]) * 16));
         }
+#pragma unroll
+        for (int pl = 0; pl < (SPLIT ? 2 : 1); pl++)
+#pragma unroll
+          for (int c = 0; c < 4; c++)
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pl], bf[c], acc[i][c], 0, 0, 0);
       }
     }
   };
 
-  // Step s computes LDS buffer s & 1 while step s + 1 loads into registers;
-  // then step s + 1 goes to the other buffer. The last step re-reads itself (unconditional: a branch would keep the
-  // staging registers in memory).
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int ks = 0; ks < ksteps; ks++) {
-    const int cur = ks & 1;
-    load(min(ks + 1, ksteps - 1));
-    compute(cur);
-    // Keep the staging work (which waits for the loads above) after the
-    // MFMAs: hoisted into them it would stall each step on the loads.
-    __builtin_amdgcn_sched_barrier(0);
-    store(cur ^ 1);
-    __syncthreads();
-  }
+  // A wave with no live units still loads its share and meets every
+  // barrier; that branch sits outside the loop (inside it, the compiler
+  // spills the accumulators around it). Loads past the last step re-read it,
+  // so every step issues the same number and the vmcnt counts hold.
+  auto mainloop = [&](auto with_mfma) {
+#pragma unroll
+    for (int j = 0; j < STAGES - 1; j++) issue(min(j, ksteps - 1), j);
+    for (int ks = 0; ks < ksteps; ks++) {
+      WAIT_VMCNT((STAGES - 2) * LOADS);  // this wave's loads of step ks
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      const int ahead = ks + STAGES - 1;
+      issue(min(ahead, ksteps - 1), ahead % STAGES);
+      if constexpr (decltype(with_mfma)::value) compute(ks % STAGES);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (live) mainloop(std::true_type{});
+  else mainloop(std::false_type{});
 
-  // ---- epilogue. acc[i][j][r]: row 32i + 8(r/4) + 4(L/32) + r%4, column
-  // L%32 of tile j.
+  // ---- epilogue. acc[i][c][r]: row 64wm + 32i + 8(r/4) + 4h + r%4,
+  // column c of this lane's unit. Outputs go through a buffer store whose
+  // offset is out of range for rows past the tile (the store is dropped):
+  // no branches, so the stores queue back to back. (Behind a per-row branch
+  // the compiler re-waits for every earlier memory access, store included,
+  // at each branch.)
+  const __amdgpu_buffer_rsrc_t orc =
+      __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.out_bytes, BUF_DWORD3);
+  auto row_off = [&](int row, int uo) -> uint32_t {
+    return row < rows ? ((uint32_t)rowmap[row] * (uint32_t)p.N + 4u * uo) * 4u : 0x80000000u;
+  };
+  // (m & x) | (~m & y) per bit: one v_bfi_b32, where a select of two
+  // elements of one accumulator vector becomes a chain over all sixteen.
+  auto pick = [](uint32_t m, float x, float y) {
+    return __builtin_bit_cast(float, (m & __builtin_bit_cast(uint32_t, x)) |
+                                         (~m & __builtin_bit_cast(uint32_t, y)));
+  };
   if (MODE == MODE_UP) {
-    const int col = ntile * 128 + 32 * wave + fr;  // glu index = lin index
-    if (col < p.N) {
-      const float sg = p.s0[(int64_t)e * p.N + col], sl = p.s1[(int64_t)e * p.N + col];
-      const float bg = p.b0 ? p.b0[(int64_t)e * p.N + col] : 0.f;
-      const float bl = p.b1 ? p.b1[(int64_t)e * p.N + col] : 0.f;
+    // Lane lm < 16 holds glu and lane lm + 16 lin of unit wu + (lm & 15):
+    // the low lane finishes rows r < 8 and the high lane rows r ≥ 8, each
+    // receiving the other projection's values for its rows from its partner.
+    const bool low = lm < 16;
+    const uint32_t lowm = low ? ~0u : 0u;
+    const int uo = min(wu + (lm & 15), N4 - 1);
+    const bool col_ok = wu + (lm & 15) < N4;
+    const int64_t so = (int64_t)e * p.N + 4 * uo;
+    const floatx4 sg = *(const floatx4 *)&p.s0[so], sl = *(const floatx4 *)&p.s1[so];
+    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+    const floatx4 bg = p.b0 ? *(const floatx4 *)&p.b0[so] : z;
+    const floatx4 bl = p.b1 ? *(const floatx4 *)&p.b1[so] : z;
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-          if (row < rows) {
-            const int64_t asg = rowmap[row];
-            p.out[asg * p.N + col] = swiglu(acc[i][0][r] * sg + bg, acc[i][1][r] * sl + bl);
-          }
+      for (int r = 0; r < 8; r++) {
+        floatx4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const float a0 = acc[i][c][r], a8 = acc[i][c][r + 8];
+          const float send = pick(lowm, a8, a0);
+          // ds_swizzle, bit mode: lane ^ 16 within each 32 lanes.
+          const float recv = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
+          const float g = pick(lowm, a0, recv);
+          const float l = pick(lowm, recv, a8);
+          v[c] = swiglu(g * sg[c] + bg[c], l * sl[c] + bl[c]);
         }
-    }
+        const int rr = low ? r : r + 8;
+        const int row = 64 * wm + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
+                                               col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
+      }
   } else {
+    const int uo = min(wu + lm, N4 - 1);
+    const bool col_ok = wu + lm < N4;
+    const int64_t so = (int64_t)e * p.N + 4 * uo;
+    const floatx4 sc = *(const floatx4 *)&p.s0[so];
+    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+    const floatx4 bb = p.b0 ? *(const floatx4 *)&p.b0[so] : z;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int col = ntile * BNW + wcol[j] + fr;
-      if (col >= p.N) continue;
-      const float sc = p.s0[(int64_t)e * p.N + col];
-      const float bb = p.b0 ? p.b0[(int64_t)e * p.N + col] : 0.f;
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int r = 0; r < 16; r++) {
+        const int row = 64 * wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+        floatx4 v;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int row = i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-          if (row < rows) {
-            const int64_t asg = rowmap[row];
-            p.out[asg * p.N + col] = acc[i][j][r] * sc + bb;
-          }
-        }
-    }
+        for (int c = 0; c < 4; c++) v[c] = acc[i][c][r] * sc[c] + bb[c];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
+                                               col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
+      }
   }
 }
 
@@ -307,8 +398,17 @@ void k_expert_gemm(GemmArgs p) {
 
 bool gemm_eligible(const ExpertArgs &ea) {
   // One scale group per column, K in whole steps.
-  const int bk = ea.a_dtype == MOE_F16 ? 64 : 32;
-  return ea.bits == 8 && ea.g == ea.K && ea.K % bk == 0 && ea.N % 4 == 0;
+  // 32-bit buffer offsets: one expert's weights and the whole input stay
+  // below 2 GiB.
+  const int64_t a_bytes = (int64_t)(ea.A / ea.a_row_div) * ea.K * (ea.a_dtype == MOE_F16 ? 2 : 4);
+  // The epilogue reads scales and biases and writes outputs 16 bytes at a
+  // time.
+  auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  const bool aligned = a16(ea.out) && a16(ea.w0.scales) && a16(ea.w0.bias) &&
+                       (ea.mode != MODE_UP || (a16(ea.w1.scales) && a16(ea.w1.bias)));
+  const int64_t out_bytes = (int64_t)ea.A * ea.N * 4;
+  return aligned && out_bytes < (1ll << 31) && ea.bits == 8 && ea.g == ea.K && ea.K % BK == 0 && ea.N % 4 == 0 &&
+         (int64_t)ea.K * ea.N < (1ll << 31) && a_bytes < (1ll << 31);
 }
 
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
@@ -317,20 +417,24 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   GemmArgs p;
   p.a = ea.a;
   p.a_row_div = ea.a_row_div;
+  p.a_bytes = (int)((int64_t)(ea.A / ea.a_row_div) * ea.K * (ea.a_dtype == MOE_F16 ? 2 : 4));
   p.w0 = ea.w0.w;
   p.s0 = ea.w0.scales;
   p.b0 = ea.w0.bias;
-  p.w1 = ea.w1.w;
-  p.s1 = ea.w1.scales;
-  p.b1 = ea.w1.bias;
+  // Down reads its one weight through both sources (units 0..63 and 64..127
+  // of the tile).
+  p.w1 = ea.mode == MODE_UP ? ea.w1.w : ea.w0.w;
+  p.s1 = ea.mode == MODE_UP ? ea.w1.scales : ea.w0.scales;
+  p.b1 = ea.mode == MODE_UP ? ea.w1.bias : ea.w0.bias;
   p.K = ea.K;
   p.N = ea.N;
   p.E = ea.E;
   p.out = ea.out;
+  p.out_bytes = (int)((int64_t)ea.A * ea.N * 4);
   p.perm = db.perm;
   p.active = db.active;
   p.meta = db.meta;
-  const int cols = ea.mode == MODE_UP ? BNW / 2 : BNW;  // output columns per tile
+  const int cols = ea.mode == MODE_UP ? 256 : 512;  // output columns per tile
   p.nt = (ea.N + cols - 1) / cols;
   // Upper bound of M-tiles over all experts: each active expert adds at most
   // one partial tile.
@@ -339,7 +443,7 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   // is a bijection; the extra blocks find no tile and exit.
   const long blocks = ((long)a_tiles * p.nt + 7) / 8 * 8;
   if (blocks > 0x7fffffffL) return moe_fail(MOE_INVALID_ARGUMENT, "expert gemm: grid too large");
-  dim3 grid((unsigned)blocks), block(256);
+  dim3 grid((unsigned)blocks), block(512);
   if (ea.mode == MODE_UP) {
     if (ea.a_dtype == MOE_F16)
       hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16>), grid, block, 0, s, p);
