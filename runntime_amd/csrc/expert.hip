@@ -455,6 +455,7 @@ __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s], slots in order; rows of
 // ids that are not experts contribute nothing. Reads, never scatters.
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, int64_t y_cs,
+                                                 int parts, int64_t part_cs,
                                                  const float *__restrict__ route, int64_t route_cs,
                                                  const float *__restrict__ residual, int64_t res_cs,
                                                  int T, int N, int E, int k,
@@ -470,7 +471,9 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
     const int64_t asg = (int64_t)t * k + s;
     if (route_expert(route, asg, k, E) < 0) continue;
     const float gate = route[(int64_t)t * 2 * k + k + s];
-    acc = fmaf(gate, y[asg * N + n], acc);
+    float v = y[asg * N + n];
+    for (int q = 1; q < parts; q++) v += y[q * part_cs + asg * N + n];
+    acc = fmaf(gate, v, acc);
   }
   out[call * out_cs + (int64_t)t * N + n] = acc;
 }
@@ -539,6 +542,14 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
 
 }  // namespace
 
+bool expert_uses_gemm(const ExpertArgs &ea) {
+  // Prefill shapes (≥ 64 rows per expert on average): the grouped GEMM.
+  static const int env_gemm = getenv("MOE_GEMM") ? atoi(getenv("MOE_GEMM")) : -1;
+  const int max_active = ea.E < ea.A ? ea.E : ea.A;
+  const bool want_gemm = env_gemm >= 0 ? env_gemm != 0 : ea.A >= 64 * max_active;
+  return ea.calls == 1 && want_gemm && gemm_eligible(ea);
+}
+
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   MOE_NONNULL(ea.a);
   MOE_NONNULL(ea.route);
@@ -555,11 +566,9 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   MOE_NONNULL(db.meta);
   if (db.E != ea.E || db.A != ea.A)
     return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch workspace sized for another shape");
-  // Prefill shapes (≥ 64 rows per expert on average): the grouped GEMM.
-  static const int env_gemm = getenv("MOE_GEMM") ? atoi(getenv("MOE_GEMM")) : -1;
-  const int max_active = ea.E < ea.A ? ea.E : ea.A;
-  const bool want_gemm = env_gemm >= 0 ? env_gemm != 0 : ea.A >= 64 * max_active;
-  if (ea.calls == 1 && want_gemm && gemm_eligible(ea)) return launch_expert_gemm(ea, db, s);
+  if (expert_uses_gemm(ea)) return launch_expert_gemm(ea, db, s);
+  if (ea.dispatch_order)
+    return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch-order rows need the grouped GEMM");
   ExpertKArgs p;
   p.a = ea.a;
   p.a_cs = ea.a_cs;
@@ -591,15 +600,16 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   return launch_mode<MODE_DOWN>(ea, p, s);
 }
 
-int launch_combine(const float *y, int64_t y_cs, const float *route, int64_t route_cs,
+int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, const float *route,
+                   int64_t route_cs,
                    const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
                    int64_t out_cs, int calls, hipStream_t s) {
   MOE_NONNULL(y);
   MOE_NONNULL(route);
   MOE_NONNULL(out);
   dim3 grid(T, (N + 255) / 256, calls), block(256);
-  hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, route, route_cs, residual, res_cs, T,
-                     N, E, k, out, out_cs);
+  hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs, route,
+                     route_cs, residual, res_cs, T, N, E, k, out, out_cs);
   return 0;
 }
 

@@ -73,6 +73,8 @@ constexpr int BK = 32;           // k per step
 constexpr int TPS = BK / 4;      // quantW tiles per unit per step
 constexpr int SLOTS = 128;       // weight units per block (2 sources × 64)
 constexpr int W_BYTES = SLOTS * TPS * 16;  // weights of one step: 16 KB
+// Largest active-expert count (descriptors cached in LDS).
+constexpr int GEMM_MAX_E = 256;
 // Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format).
 constexpr int BUF_DWORD3 = 0x00020000;
 
@@ -90,9 +92,14 @@ struct GemmArgs {
   float *out;
   int out_bytes;  // size of out (bounds of its buffer stores)
   const int32_t *perm;
+  int perm_bytes;
   const int32_t *active;  // [E][4] {e, first row, rows, first M-tile}
   const int32_t *meta;
   int nt;                 // N-tiles
+  int sorted;             // act in dispatch order: up writes row r0 + row, down reads it
+  int parts;              // K parts (down); part q writes out + q·A·N
+  int kpart;              // steps per part
+  int part_floats;        // A·N
 };
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
@@ -140,8 +147,34 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void *base, uint32_t bytes) {
   return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, BUF_DWORD3};
 }
 
-// s_waitcnt with vmcnt = n (< 16) and no wait on the other counters.
-#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
+// The same for 4 bytes per lane (LDS at lds_addr + 4·lane).
+__device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, int soff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr) : "memory");
+}
+
+// s_waitcnt with vmcnt = n (< 64) and no wait on the other counters.
+#define WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// Workgroup barrier without a memory fence (a fence would wait for every
+// load in flight); the asm statements keep the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One tile of the grouped GEMM, uniform across the block.
+struct Tile {
+  int e;     // expert
+  int r0;    // first sorted row (dispatch order) of the tile
+  int rows;  // rows of the tile (≤ BM)
+  int U0, U1;  // first unit of each weight source
+  int part;  // K part
+  int kb;    // first step of the part
+};
 
 template <int MODE, typename AT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
@@ -150,50 +183,106 @@ void k_expert_gemm(GemmArgs p) {
   constexpr int A_BYTES = BM * BK * (int)sizeof(AT);  // 8 or 16 KB
   constexpr int STAGE = W_BYTES + A_BYTES;
   constexpr int STAGES = SPLIT ? 4 : 6;               // 128 or 144 KB
-  constexpr int LOADS = SPLIT ? 4 : 3;                // per thread per step
+  constexpr int LOADS = SPLIT ? 4 : 3;                // ring loads per lane per step
+  constexpr int TILE_LOADS = 2;                       // row map + constants, per lane per tile
+  constexpr int STORES = MODE == MODE_UP ? 16 : 32;   // epilogue stores per lane
+  constexpr int BASE_WAIT = (STAGES - 2) * LOADS;
   __shared__ __align__(16) uint8_t lds[STAGES * STAGE];
-  __shared__ int32_t rowmap[BM];  // assignment of each tile row
+  __shared__ __align__(16) int32_t rowmap[2][BM];     // assignment of each tile row
+  // Per-tile epilogue constants: up → glu scales, lin scales, glu biases,
+  // lin biases (256 each); down → scales, biases (512 each).
+  __shared__ __align__(16) float consts[2][1024];
+  __shared__ int4 descs[GEMM_MAX_E];                  // active-expert descriptors
 
-  // ---- which tile: XCD-contiguous block order (gridDim.x is a multiple of
-  // 8), then expert / N / M.
-  const int nblk = gridDim.x;
-  const int b = blockIdx.x;
-  const int per_xcd = nblk / 8;
-  const int L = (b % 8) * per_xcd + b / 8;
-  const int total_tiles = p.meta[META_TILES];
-  if (L >= total_tiles * p.nt) return;
+  // ---- this block's tiles. The tile list (expert, then N-tile, then
+  // M-tile) is cut into 8 contiguous ranges, one per XCD (block b runs on
+  // XCD b mod 8); the XCD's blocks take its tiles round robin, so the tiles
+  // in flight on one XCD at a time are neighbours that share weights.
+  const int total = p.meta[META_TILES] * p.nt * p.parts;
   const int n_active = p.meta[META_ACTIVE];
-  const int t = L / p.nt;  // global M-tile index of this tile's expert range
-  int lo = 0, hi = n_active - 1;
-  while (lo < hi) {  // last active expert whose first M-tile ≤ t
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.active[4 * mid + 3] <= t) lo = mid; else hi = mid - 1;
-  }
-  const int4 desc = ((const int4 *)p.active)[lo];
-  const int e = desc.x, row0 = desc.y, cnt = desc.z, tile0 = desc.w;
-  const int mt = (cnt + BM - 1) / BM;
-  const int local = L - tile0 * p.nt;
-  const int ntile = local / mt;
-  const int mtile = local % mt;
-  const int m0 = mtile * BM;
-  const int rows = min(BM, cnt - m0);
+  const int bx = gridDim.x >> 3;  // blocks per XCD
+  const int xcd = blockIdx.x & 7, xb = blockIdx.x >> 3;
+  const int per_x = (total + 7) >> 3;
+  const int start = xcd * per_x + xb, end = min(total, (xcd + 1) * per_x);
+  if (start >= end) return;
+  const int ntiles = (end - start + bx - 1) / bx;
 
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform
-  const int wm = wave & 1, wn = wave >> 1;
+  // Wavefront w runs on SIMD w % 4, so each SIMD holds one wavefront of
+  // each row half: a tile of at most 64 rows, whose second half skips its
+  // MFMAs, leaves every SIMD one busy wavefront instead of idling two.
+  const int wm = wave >> 2, wn = wave & 3;
+  const int lm = lane & 31, h = lane >> 5;
   const int N4 = p.N / 4;
-  const int ksteps = p.K / BK;
-  // First unit of each source.
-  const int U0 = MODE == MODE_UP ? ntile * 64 : ntile * 128;
-  const int U1 = MODE == MODE_UP ? ntile * 64 : ntile * 128 + 64;
+  const int ksteps = p.kpart;  // steps per tile
 
-  if (tid < BM) rowmap[tid] = p.perm[row0 + m0 + min(tid, rows - 1)];
+  for (int i = tid; i < n_active; i += blockDim.x) descs[i] = ((const int4 *)p.active)[i];
   __syncthreads();
 
-  // ---- this wavefront's loads of a step. Each load instruction fills 1 KB
-  // of LDS (lane l at +16·l), so lane l picks the global chunk that belongs
-  // at that position.
+  // Tile L: expert (by its M-tile range), then N-tile, then K part, then
+  // M-tile.
+  const int ntp = p.nt * p.parts;
+  auto tile_at = [&](int L) {
+    const int t = L / ntp;  // global M-tile index within the tile's expert range
+    int lo = 0, hi = n_active - 1;
+    while (lo < hi) {  // last active expert whose first M-tile ≤ t
+      const int mid = (lo + hi + 1) >> 1;
+      if (descs[mid].w <= t) lo = mid; else hi = mid - 1;
+    }
+    const int4 d = descs[lo];
+    const int mt = (d.z + BM - 1) / BM;
+    const int local = L - d.w * ntp;
+    const int ntile = local / (mt * p.parts), rem = local % (mt * p.parts);
+    const int part = rem / mt, mtile = rem % mt;
+    Tile T;
+    T.e = __builtin_amdgcn_readfirstlane(d.x);
+    T.r0 = __builtin_amdgcn_readfirstlane(d.y + mtile * BM);
+    T.rows = __builtin_amdgcn_readfirstlane(min(BM, d.z - mtile * BM));
+    T.U0 = __builtin_amdgcn_readfirstlane(MODE == MODE_UP ? ntile * 64 : ntile * 128);
+    T.U1 = __builtin_amdgcn_readfirstlane(MODE == MODE_UP ? ntile * 64 : ntile * 128 + 64);
+    T.part = __builtin_amdgcn_readfirstlane(part);
+    T.kb = __builtin_amdgcn_readfirstlane(part * p.kpart);
+    return T;
+  };
+
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
+  const uint32_t rowmap0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t *)&rowmap[0][0];
+  const uint32_t consts0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)&consts[0][0];
+  const uint32_t slab = (uint32_t)p.K * (uint32_t)p.N;  // weight bytes of one expert
+  const i32x4 ar = buffer_rsrc(p.a, (uint32_t)p.a_bytes);
+  const i32x4 pr = buffer_rsrc(p.perm, (uint32_t)p.perm_bytes);
+  // Constants this wavefront loads per tile: up → array wave/2 (glu scales,
+  // lin scales, glu biases, lin biases), half wave & 1; down → array wave/4
+  // (scales, biases), quarter wave & 3. A missing bias reads zeros (an empty
+  // buffer).
+  const float *cbase = MODE == MODE_UP
+                           ? (wave < 2 ? p.s0 : wave < 4 ? p.s1 : wave < 6 ? p.b0 : p.b1)
+                           : (wave < 4 ? p.s0 : p.b0);
+  const i32x4 cr = buffer_rsrc(cbase, cbase ? (uint32_t)p.E * (uint32_t)p.N * 4u : 0u);
+
+  // ---- per-tile loads into LDS buffer `sel`: the row map (perm entries of
+  // rows 16·wave + l, l < 16; rows past the tile repeat its last) and the
+  // epilogue constants (512 bytes per wavefront, lanes 0-31). One load
+  // instruction each per wavefront.
+  auto issue_tile = [&](const Tile &T, int sel) {
+    if (lane < 16) {
+      const int r = 16 * wave + lane;
+      dma4(pr, (uint32_t)(T.r0 + min(r, T.rows - 1)) * 4u, 0, rowmap0 + sel * (BM * 4) + 64 * wave);
+    }
+    if (lane < 32) {
+      const int col = 4 * T.U0 + (MODE == MODE_UP ? (wave & 1) : (wave & 3)) * 128 + 4 * lane;
+      dma16(cr, ((uint32_t)T.e * (uint32_t)p.N + (uint32_t)col) * 4u, 0,
+            consts0 + sel * 4096 + 512 * wave);
+    }
+  };
+
+  // ---- ring loads of a step. Each load instruction fills 1 KB of LDS
+  // (lane l at +16·l), so lane l picks the global chunk that belongs at that
+  // position.
   // Weights: instructions i = 0, 1 fill slots 16·wave + 8i .. +7 (wavefronts
   // 0-3: source 0, 4-7: source 1); lane l: slot + (l >> 3), position l & 7
   // holds tile (l & 7) ^ sw8(slot). A unit past N gets an offset past the
@@ -203,54 +292,51 @@ void k_expert_gemm(GemmArgs p) {
   //    16·wave + 8i + (l >> 3), position l & 7 holds 4-float chunk
   //    (l & 7) ^ sw8(row). Rows past the tile's read its last row: MFMA rows
   //    are independent and the epilogue writes none of them.
-  const uint32_t slab = (uint32_t)p.K * (uint32_t)p.N;  // bytes of one expert
-  const i32x4 wr = buffer_rsrc((wave < 4 ? p.w0 : p.w1) + (int64_t)e * (slab / 4), slab);
-  const i32x4 ar = buffer_rsrc(p.a, (uint32_t)p.a_bytes);
-  // LDS byte address of the ring.
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds;
-  uint32_t woff[2];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int slot = 16 * wave + 8 * i + (lane >> 3);
-    const int u = (wave < 4 ? U0 : U1) + (slot & 63);
-    const int tile = (lane & 7) ^ sw8(slot);
-    woff[i] = u < N4 ? (uint32_t)u * (uint32_t)p.K * 4u + tile * 16u : 0x80000000u;
-  }
   constexpr int AI = SPLIT ? 2 : 1;
-  uint32_t aoffg[AI];
+  struct Params {
+    i32x4 wr;
+    uint32_t woff[2], aoff[AI];
+  };
+  auto make_params = [&](const Tile &T, int sel) {
+    Params P;
+    P.wr = buffer_rsrc((wave < 4 ? p.w0 : p.w1) + (int64_t)T.e * (slab / 4), slab);
 #pragma unroll
-  for (int i = 0; i < AI; i++) {
-    if (SPLIT) {
-      const int r = 16 * wave + 8 * i + (lane >> 3);
-      const uint32_t srow = (uint32_t)(rowmap[r] / p.a_row_div);
-      aoffg[i] = srow * (uint32_t)p.K * 4u + ((lane & 7) ^ sw8(r)) * 16u;
-    } else {
-      const int r = 16 * wave + (lane >> 2);
-      const uint32_t srow = (uint32_t)(rowmap[r] / p.a_row_div);
-      aoffg[i] = srow * (uint32_t)p.K * 2u + ((lane & 3) ^ sw4(r)) * 16u;
+    for (int i = 0; i < 2; i++) {
+      const int slot = 16 * wave + 8 * i + (lane >> 3);
+      const int u = (wave < 4 ? T.U0 : T.U1) + (slot & 63);
+      const int tile = (lane & 7) ^ sw8(slot);
+      P.woff[i] = u < N4 ? (uint32_t)u * (uint32_t)p.K * 4u + tile * 16u : 0x80000000u;
     }
-  }
-  auto issue = [&](int ks, int stage) {
+#pragma unroll
+    for (int i = 0; i < AI; i++) {
+      if (SPLIT) {
+        const int r = 16 * wave + 8 * i + (lane >> 3);
+        const uint32_t srow = MODE == MODE_DOWN && p.sorted ? (uint32_t)(T.r0 + min(r, T.rows - 1))
+                                       : (uint32_t)(rowmap[sel][r] / p.a_row_div);
+        P.aoff[i] = srow * (uint32_t)p.K * 4u + ((lane & 7) ^ sw8(r)) * 16u;
+      } else {
+        const int r = 16 * wave + (lane >> 2);
+        const uint32_t srow = MODE == MODE_DOWN && p.sorted ? (uint32_t)(T.r0 + min(r, T.rows - 1))
+                                       : (uint32_t)(rowmap[sel][r] / p.a_row_div);
+        P.aoff[i] = srow * (uint32_t)p.K * 2u + ((lane & 3) ^ sw4(r)) * 16u;
+      }
+    }
+    return P;
+  };
+  auto issue = [&](const Params &P, int ks, int stage) {
     const uint32_t st = lds0 + stage * STAGE;
 #pragma unroll
-    for (int i = 0; i < 2; i++) dma16(wr, woff[i], ks * (TPS * 16), st + (2 * wave + i) * 1024);
+    for (int i = 0; i < 2; i++) dma16(P.wr, P.woff[i], ks * (TPS * 16), st + (2 * wave + i) * 1024);
 #pragma unroll
     for (int i = 0; i < AI; i++)
-      dma16(ar, aoffg[i], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + i) * 1024);
+      dma16(ar, P.aoff[i], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + i) * 1024);
   };
 
   floatx16 acc[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
   // Fragment positions. B: this lane's slot (up: glu unit 16·wn + (lm & 15)
   // for lm < 16, the same lin unit for lm ≥ 16; down: slot 32·wn + lm),
   // tiles 4h + 2kk (+1). A: rows 64·wm + 32i + lm, k 16h + 8kk .. +7.
-  const int lm = lane & 31, h = lane >> 5;
   const int slot = MODE == MODE_UP ? (lm < 16 ? 0 : 64) + 16 * wn + (lm & 15) : 32 * wn + lm;
   const int boff = slot * 128, bsw = sw8(slot);
   int aoff[2], asw[2];
@@ -260,10 +346,6 @@ void k_expert_gemm(GemmArgs p) {
     aoff[i] = W_BYTES + arow * BK * (int)sizeof(AT);
     asw[i] = SPLIT ? sw8(arow) : sw4(arow);
   }
-  // First unit of this wavefront (both halves for up).
-  const int wu = MODE == MODE_UP ? U0 + 16 * wn : (wn < 2 ? U0 : U1) + 32 * (wn & 1);
-  // Waves whose units are all past N skip the MFMAs (uniform per wave).
-  const bool live = wu < N4;
 
   auto compute = [&](int stage) {
     const uint8_t *st = lds + stage * STAGE;
@@ -300,115 +382,188 @@ void k_expert_gemm(GemmArgs p) {
     }
   };
 
-  // A wave with no live units still loads its share and meets every
-  // barrier; that branch sits outside the loop (inside it, the compiler
-  // spills the accumulators around it). Loads past the last step re-read it,
-  // so every step issues the same number and the vmcnt counts hold.
-  auto mainloop = [&](auto with_mfma) {
-#pragma unroll
-    for (int j = 0; j < STAGES - 1; j++) issue(min(j, ksteps - 1), j);
-    for (int ks = 0; ks < ksteps; ks++) {
-      WAIT_VMCNT((STAGES - 2) * LOADS);  // this wave's loads of step ks
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      const int ahead = ks + STAGES - 1;
-      issue(min(ahead, ksteps - 1), ahead % STAGES);
-      if constexpr (decltype(with_mfma)::value) compute(ks % STAGES);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  if (live) mainloop(std::true_type{});
-  else mainloop(std::false_type{});
-
-  // ---- epilogue. acc[i][c][r]: row 64wm + 32i + 8(r/4) + 4h + r%4,
-  // column c of this lane's unit. Outputs go through a buffer store whose
-  // offset is out of range for rows past the tile (the store is dropped):
-  // no branches, so the stores queue back to back. (Behind a per-row branch
-  // the compiler re-waits for every earlier memory access, store included,
-  // at each branch.)
+  // ---- epilogue of tile T from LDS buffer `sel`. acc[i][c][r]: row
+  // 64wm + 32i + 8(r/4) + 4h + r%4, column c of this lane's unit. Outputs go
+  // through a buffer store whose offset is out of range for rows past the
+  // tile (the store is dropped): no branches, so the stores queue back to
+  // back. (Behind a per-row branch the compiler re-waits for every earlier
+  // memory access, store included, at each branch.)
   const __amdgpu_buffer_rsrc_t orc =
       __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.out_bytes, BUF_DWORD3);
-  auto row_off = [&](int row, int uo) -> uint32_t {
-    return row < rows ? ((uint32_t)rowmap[row] * (uint32_t)p.N + 4u * uo) * 4u : 0x80000000u;
-  };
   // (m & x) | (~m & y) per bit: one v_bfi_b32, where a select of two
   // elements of one accumulator vector becomes a chain over all sixteen.
   auto pick = [](uint32_t m, float x, float y) {
     return __builtin_bit_cast(float, (m & __builtin_bit_cast(uint32_t, x)) |
                                          (~m & __builtin_bit_cast(uint32_t, y)));
   };
-  if (MODE == MODE_UP) {
-    // Lane lm < 16 holds glu and lane lm + 16 lin of unit wu + (lm & 15):
-    // the low lane finishes rows r < 8 and the high lane rows r ≥ 8, each
-    // receiving the other projection's values for its rows from its partner.
-    const bool low = lm < 16;
-    const uint32_t lowm = low ? ~0u : 0u;
-    const int uo = min(wu + (lm & 15), N4 - 1);
-    const bool col_ok = wu + (lm & 15) < N4;
-    const int64_t so = (int64_t)e * p.N + 4 * uo;
-    const floatx4 sg = *(const floatx4 *)&p.s0[so], sl = *(const floatx4 *)&p.s1[so];
-    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-    const floatx4 bg = p.b0 ? *(const floatx4 *)&p.b0[so] : z;
-    const floatx4 bl = p.b1 ? *(const floatx4 *)&p.b1[so] : z;
+  auto epilogue = [&](const Tile &T, int wu, int sel) {
+    // Up with sorted rows writes act at the dispatch position.
+    const bool out_sorted = MODE == MODE_UP && p.sorted;
+    auto row_off = [&](int row, int uo) -> uint32_t {
+      const uint32_t orow = out_sorted ? (uint32_t)(T.r0 + row) : (uint32_t)rowmap[sel][row];
+      return row < T.rows ? (orow * (uint32_t)p.N + 4u * uo) * 4u : 0x80000000u;
+    };
+    const float *cs = consts[sel];
+    if (MODE == MODE_UP) {
+      // Lane lm < 16 holds glu and lane lm + 16 lin of unit wu + (lm & 15):
+      // the low lane finishes rows r < 8 and the high lane rows r ≥ 8, each
+      // receiving the other projection's values for its rows from its
+      // partner.
+      const bool low = lm < 16;
+      const uint32_t lowm = low ? ~0u : 0u;
+      const int uo = wu + (lm & 15);
+      const bool col_ok = uo < N4;
+      const int q = 4 * (uo - T.U0);  // output index within the tile
+      const floatx4 sg = *(const floatx4 *)&cs[q], sl = *(const floatx4 *)&cs[256 + q];
+      const floatx4 bg = *(const floatx4 *)&cs[512 + q], bl = *(const floatx4 *)&cs[768 + q];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int r = 0; r < 8; r++) {
-        floatx4 v;
+        for (int r = 0; r < 8; r++) {
+          floatx4 v;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const float a0 = acc[i][c][r], a8 = acc[i][c][r + 8];
-          const float send = pick(lowm, a8, a0);
-          // ds_swizzle, bit mode: lane ^ 16 within each 32 lanes.
-          const float recv = __builtin_bit_cast(
-              float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
-          const float g = pick(lowm, a0, recv);
-          const float l = pick(lowm, recv, a8);
-          v[c] = swiglu(g * sg[c] + bg[c], l * sl[c] + bl[c]);
+          for (int c = 0; c < 4; c++) {
+            const float a0 = acc[i][c][r], a8 = acc[i][c][r + 8];
+            const float send = pick(lowm, a8, a0);
+            // ds_swizzle, bit mode: lane ^ 16 within each 32 lanes.
+            const float recv = __builtin_bit_cast(
+                float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
+            const float g = pick(lowm, a0, recv);
+            const float l = pick(lowm, recv, a8);
+            v[c] = swiglu(g * sg[c] + bg[c], l * sl[c] + bl[c]);
+          }
+          const int rr = low ? r : r + 8;
+          const int row = 64 * wm + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
+                                                 col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
         }
-        const int rr = low ? r : r + 8;
-        const int row = 64 * wm + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
-                                               col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
-      }
-  } else {
-    const int uo = min(wu + lm, N4 - 1);
-    const bool col_ok = wu + lm < N4;
-    const int64_t so = (int64_t)e * p.N + 4 * uo;
-    const floatx4 sc = *(const floatx4 *)&p.s0[so];
-    const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-    const floatx4 bb = p.b0 ? *(const floatx4 *)&p.b0[so] : z;
+    } else {
+      const int uo = wu + lm;
+      const bool col_ok = uo < N4;
+      const int q = 4 * (uo - T.U0);
+      // The bias goes into part 0 only; every part carries its scale.
+      const floatx4 sc = *(const floatx4 *)&cs[q];
+      const floatx4 bb = *(const floatx4 *)&cs[512 + q] * (T.part == 0 ? 1.f : 0.f);
+      const uint32_t pbase = (uint32_t)T.part * (uint32_t)p.part_floats * 4u;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = 64 * wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+          floatx4 v;
+#pragma unroll
+          for (int c = 0; c < 4; c++) v[c] = acc[i][c][r] * sc[c] + bb[c];
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
+                                                 col_ok ? row_off(row, uo) + pbase : 0x80000000u, 0, 0);
+        }
+    }
+  };
+
+  // ---- the pipeline. Ring loads run STAGES − 1 steps ahead of the MFMAs,
+  // across tile boundaries: the first steps of tile j + 1 load while tile j
+  // finishes and stores. The row map and constants of tile j + 1 load
+  // STAGES − 1 steps before its first ring load needs the row map. Each step
+  // waits (vmcnt) for this wavefront's ring loads of the step; the
+  // threshold counts what was issued after them: the ring loads of the next
+  // STAGES − 2 steps, plus the previous tile's epilogue stores in the first
+  // steps of a tile, plus the next tile's row map and constants while those
+  // are younger. The loop issues the same number of ring loads every step
+  // (past the last tile it re-reads the last step), so the counts hold.
+  Tile cur = tile_at(start), nxt = cur;
+  issue_tile(cur, 0);
+  WAIT_VMCNT(0);
+  block_barrier();
+  Params pc = make_params(cur, 0), pn = pc;
+  if (ntiles > 1) nxt = tile_at(start + bx);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; s++) issue(pc, cur.kb + s, s);
+  const int tile_step = ksteps - 2 * STAGES + 2;  // ≥ STAGES − 2 (checked on the host)
+  int stage = 0;
+  for (int j = 0; j < ntiles; j++) {
+    const bool has_next = j + 1 < ntiles;
+    const int sel = j & 1;
+    const int wu = MODE == MODE_UP ? cur.U0 + 16 * wn : (wn < 2 ? cur.U0 : cur.U1) + 32 * (wn & 1);
+    // Uniform: waves with no unit below N or no row in the tile skip the MFMAs.
+    const bool live = wu < N4 && 64 * wm < cur.rows;
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = 64 * wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-        floatx4 v;
+      for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = acc[i][c][r] * sc[c] + bb[c];
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
-                                               col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
-      }
+        for (int r = 0; r < 16; r++) acc[i][c][r] = 0.f;
+    for (int ks = 0; ks < ksteps; ks++) {
+      if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(BASE_WAIT + STORES);
+      else if (has_next && ks > tile_step && ks <= tile_step + STAGES - 2) WAIT_VMCNT(BASE_WAIT + TILE_LOADS);
+      else WAIT_VMCNT(BASE_WAIT);
+      block_barrier();
+      if (has_next && ks == tile_step) issue_tile(nxt, sel ^ 1);
+      if (has_next && ks == ksteps - STAGES + 1) pn = make_params(nxt, sel ^ 1);
+      const int ahead = ks + STAGES - 1;
+      const int astage = stage == 0 ? STAGES - 1 : stage - 1;
+      if (ahead < ksteps) issue(pc, cur.kb + ahead, astage);
+      else if (has_next) issue(pn, nxt.kb + ahead - ksteps, astage);
+      else issue(pc, cur.kb + ksteps - 1, astage);
+      if (live) compute(stage);
+      __builtin_amdgcn_sched_barrier(0);
+      stage = stage + 1 == STAGES ? 0 : stage + 1;
+    }
+    epilogue(cur, wu, sel);
+    if (has_next) {
+      cur = nxt;
+      pc = pn;
+      if (j + 2 < ntiles) nxt = tile_at(start + (j + 2) * bx);
+    }
   }
+  // The last steps' ring loads (re-reads) still write LDS: let them land
+  // before the workgroup's LDS is released.
+  WAIT_VMCNT(0);
 }
 
 }  // namespace
 
+static int gemm_stages(const ExpertArgs &ea) { return ea.a_dtype == MOE_F16 ? 6 : 4; }
+
 bool gemm_eligible(const ExpertArgs &ea) {
-  // One scale group per column, K in whole steps.
-  // 32-bit buffer offsets: one expert's weights and the whole input stay
-  // below 2 GiB.
+  // One scale group per column, K in whole steps, 32-bit buffer offsets
+  // (one expert's weights, the input, the scales and the outputs stay below
+  // 2 GiB), and enough steps per tile for the ring: the next tile's row map
+  // loads 2·STAGES − 2 steps before the end of a tile, after the previous
+  // epilogue's stores have left the wait window.
   const int64_t a_bytes = (int64_t)(ea.A / ea.a_row_div) * ea.K * (ea.a_dtype == MOE_F16 ? 2 : 4);
-  // The epilogue reads scales and biases and writes outputs 16 bytes at a
-  // time.
-  auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
-  const bool aligned = a16(ea.out) && a16(ea.w0.scales) && a16(ea.w0.bias) &&
-                       (ea.mode != MODE_UP || (a16(ea.w1.scales) && a16(ea.w1.bias)));
-  const int64_t out_bytes = (int64_t)ea.A * ea.N * 4;
-  return aligned && out_bytes < (1ll << 31) && ea.bits == 8 && ea.g == ea.K && ea.K % BK == 0 && ea.N % 4 == 0 &&
-         (int64_t)ea.K * ea.N < (1ll << 31) && a_bytes < (1ll << 31);
+  const int64_t out_bytes = (int64_t)ea.A * ea.N * 4 * (ea.mode == MODE_DOWN ? 2 : 1);
+  return ea.bits == 8 && ea.g == ea.K && ea.K % BK == 0 && ea.N % 4 == 0 &&
+         ea.K / BK >= 3 * gemm_stages(ea) && ea.E <= GEMM_MAX_E && out_bytes < (1ll << 31) &&
+         (int64_t)ea.K * ea.N < (1ll << 31) && a_bytes < (1ll << 31) &&
+         (int64_t)ea.E * ea.N * 4 < (1ll << 31) && (int64_t)ea.A * 4 < (1ll << 31);
+}
+
+static int gemm_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus[dev];
+}
+
+// Upper bound of the M-tiles over all experts: each active expert adds at
+// most one partial tile.
+static long gemm_mtiles(const ExpertArgs &ea) {
+  return (ea.A + BM - 1) / BM + (ea.E < ea.A ? ea.E : ea.A);
+}
+
+int gemm_down_parts(const ExpertArgs &ea) {
+  if (ea.mode != MODE_DOWN || !gemm_eligible(ea)) return 1;
+  const int ksteps = ea.K / BK;
+  if (ksteps % 2 || ksteps / 2 < 3 * gemm_stages(ea)) return 1;
+  const long cus = gemm_cus();
+  if (cus <= 0) return 1;
+  // Rounds of whole tiles over the CUs against rounds of half tiles (each
+  // half as long), from the upper bound of the tile count.
+  const long tiles = gemm_mtiles(ea) * ((ea.N + 511) / 512);
+  const long whole = (tiles + cus - 1) / cus;
+  const long halves = (2 * tiles + cus - 1) / cus;
+  return halves < 2 * whole ? 2 : 1;
 }
 
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
@@ -430,19 +585,26 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   p.N = ea.N;
   p.E = ea.E;
   p.out = ea.out;
-  p.out_bytes = (int)((int64_t)ea.A * ea.N * 4);
+  p.out_bytes = (int)((int64_t)ea.A * ea.N * 4 * (ea.mode == MODE_DOWN && ea.parts == 2 ? 2 : 1));
   p.perm = db.perm;
+  p.perm_bytes = ea.A * 4;
+  p.sorted = ea.dispatch_order;
   p.active = db.active;
   p.meta = db.meta;
   const int cols = ea.mode == MODE_UP ? 256 : 512;  // output columns per tile
   p.nt = (ea.N + cols - 1) / cols;
-  // Upper bound of M-tiles over all experts: each active expert adds at most
-  // one partial tile.
-  const int a_tiles = (ea.A + BM - 1) / BM + (ea.E < ea.A ? ea.E : ea.A);
-  // A multiple of 8 blocks, so the XCD-contiguous renumbering in the kernel
-  // is a bijection; the extra blocks find no tile and exit.
-  const long blocks = ((long)a_tiles * p.nt + 7) / 8 * 8;
-  if (blocks > 0x7fffffffL) return moe_fail(MOE_INVALID_ARGUMENT, "expert gemm: grid too large");
+  p.parts = ea.mode == MODE_DOWN && ea.parts == 2 ? 2 : 1;
+  p.kpart = ea.K / BK / p.parts;
+  p.part_floats = ea.A * ea.N;
+  if (p.kpart < 3 * gemm_stages(ea))
+    return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: too few steps per K part");
+  // Persistent blocks, one per CU (the LDS ring takes a CU), a multiple of 8
+  // for the XCD split; blocks past the tile count exit at once.
+  const int cus = gemm_cus();
+  if (cus <= 0) return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: no CU count for the device");
+  long blocks = gemm_mtiles(ea) * p.nt * p.parts;
+  if (blocks > cus) blocks = cus;
+  blocks = (blocks + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(512);
   if (ea.mode == MODE_UP) {
     if (ea.a_dtype == MOE_F16)

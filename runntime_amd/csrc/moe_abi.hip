@@ -384,12 +384,6 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
   if ((rc = check_weight("moeDown", down, K, N, E, bits, group_size))) return rc;
   REQUIRE(T >= 1, "moeDown: T must be at least 1");
   REQUIRE(act && route && out, "moeDown: NULL tensor");
-  LayerWs L;
-  if ((rc = plan_ws(ctx, 1, T, k, E, 0, 0, 0, (size_t)T * k * N, L))) return rc;
-  {
-    ProfScope ps(ctx, PG_DISPATCH);
-    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, ctx->stream))) return rc;
-  }
   ExpertArgs ea{};
   ea.mode = MODE_DOWN;
   ea.a = act;
@@ -403,16 +397,24 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
   ea.E = E;
   ea.bits = bits;
   ea.g = group_size;
-  ea.out = L.y;
   ea.A = T * k;
   ea.calls = 1;
+  ea.parts = expert_uses_gemm(ea) ? gemm_down_parts(ea) : 1;
+  LayerWs L;
+  if ((rc = plan_ws(ctx, 1, T, k, E, 0, 0, 0, (size_t)ea.parts * T * k * N, L))) return rc;
+  ea.out = L.y;
+  {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, ctx->stream))) return rc;
+  }
   {
     ProfScope ps(ctx, PG_DOWN);
     if ((rc = launch_expert(ea, L.db, ctx->stream))) return rc;
   }
   {
     ProfScope ps(ctx, PG_COMBINE);
-    if ((rc = launch_combine(L.y, 0, route, 0, residual, 0, T, N, E, k, out, 0, 1, ctx->stream)))
+    if ((rc = launch_combine(L.y, 0, ea.parts, (int64_t)T * k * N, route, 0, residual, 0, T, N, E,
+                             k, out, 0, 1, ctx->stream)))
       return rc;
   }
   return after_launch("moeDown");
@@ -442,32 +444,14 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
     REQUIRE(st->x != 0 && st->out != 0 && (!route_out || st->route != 0),
             "moe_layer: calls > 1 need distinct x, out and route_out (non-zero strides)");
   const int A = T * k;
-  LayerWs L;
-  if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
-                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)A * d, L)))
-    return rc;
-  float *route = route_out ? route_out : L.route;
-  const int64_t route_cs = route_out ? st->route : (int64_t)T * 2 * k;
-  hipStream_t s = ctx->stream;
-  bool dispatched = false;
-  {
-    ProfScope ps(ctx, PG_ROUTER);
-    RouterArgs ra{x, x_dtype, st->x, w_router, st->router_w, b_router, st->router_b, route,
-                  route_cs, L.partial, T, d, E, k, calls};
-    if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
-  }
-  if (!dispatched) {
-    ProfScope ps(ctx, PG_DISPATCH);
-    if ((rc = launch_dispatch(route, route_cs, T, E, k, calls, TILE_M, L.db, s))) return rc;
-  }
+  // Expert products first (without buffers), so the workspace is sized for
+  // the path they take.
   ExpertArgs up{};
   up.mode = MODE_UP;
   up.a = x;
   up.a_dtype = x_dtype;
   up.a_cs = st->x;
   up.a_row_div = k;
-  up.route = route;
-  up.route_cs = route_cs;
   up.k = k;
   up.w0 = *glu;
   up.w1 = *lin;
@@ -482,22 +466,14 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   up.E = E;
   up.bits = bits;
   up.g = group_size_up;
-  up.out = L.act;
   up.out_cs = (int64_t)A * I;
   up.A = A;
   up.calls = calls;
-  {
-    ProfScope ps(ctx, PG_UP);
-    if ((rc = launch_expert(up, L.db, s))) return rc;
-  }
   ExpertArgs dn{};
   dn.mode = MODE_DOWN;
-  dn.a = L.act;
   dn.a_dtype = MOE_F32;
   dn.a_cs = (int64_t)A * I;
   dn.a_row_div = 1;
-  dn.route = route;
-  dn.route_cs = route_cs;
   dn.k = k;
   dn.w0 = *down;
   dn.w0_cs = st->down_w;
@@ -508,18 +484,54 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   dn.E = E;
   dn.bits = bits;
   dn.g = group_size_down;
-  dn.out = L.y;
-  dn.out_cs = (int64_t)A * d;
   dn.A = A;
   dn.calls = calls;
+  // Both products on the grouped GEMM: act stays in dispatch order, so down
+  // streams each tile's rows contiguously instead of gathering them; down
+  // may split K in two partial products, which the combine adds.
+  if (expert_uses_gemm(up) && expert_uses_gemm(dn)) {
+    up.dispatch_order = dn.dispatch_order = 1;
+    dn.parts = gemm_down_parts(dn);
+  } else {
+    dn.parts = 1;
+  }
+  dn.out_cs = (int64_t)dn.parts * A * d;
+
+  LayerWs L;
+  if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
+                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L)))
+    return rc;
+  float *route = route_out ? route_out : L.route;
+  const int64_t route_cs = route_out ? st->route : (int64_t)T * 2 * k;
+  up.route = dn.route = route;
+  up.route_cs = dn.route_cs = route_cs;
+  up.out = L.act;
+  dn.a = L.act;
+  dn.out = L.y;
+  hipStream_t s = ctx->stream;
+  bool dispatched = false;
+  {
+    ProfScope ps(ctx, PG_ROUTER);
+    RouterArgs ra{x, x_dtype, st->x, w_router, st->router_w, b_router, st->router_b, route,
+                  route_cs, L.partial, T, d, E, k, calls};
+    if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
+  }
+  if (!dispatched) {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, route_cs, T, E, k, calls, TILE_M, L.db, s))) return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_UP);
+    if ((rc = launch_expert(up, L.db, s))) return rc;
+  }
   {
     ProfScope ps(ctx, PG_DOWN);
     if ((rc = launch_expert(dn, L.db, s))) return rc;
   }
   {
     ProfScope ps(ctx, PG_COMBINE);
-    if ((rc = launch_combine(L.y, (int64_t)A * d, route, route_cs, residual, st->residual, T, d,
-                             E, k, out, st->out, calls, s)))
+    if ((rc = launch_combine(L.y, dn.out_cs, dn.parts, (int64_t)A * d, route, route_cs, residual,
+                             st->residual, T, d, E, k, out, st->out, calls, s)))
       return rc;
   }
   return after_launch("moe_layer");
@@ -546,6 +558,7 @@ extern "C" int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, in
   REQUIRE(calls >= 1 && T >= 1 && d >= 1 && I >= 1 && E >= 1 && k >= 1,
           "moe_ctx_reserve: sizes must be positive");
   LayerWs L;
+  // y: room for down's two K parts (the grouped GEMM may split K).
   return plan_ws(ctx, calls, T, k, E, (size_t)T * 2 * k, router_partial_floats(T, d, E),
-                 (size_t)T * k * I, (size_t)T * k * (d > I ? d : I), L);
+                 (size_t)T * k * I, (size_t)2 * T * k * (d > I ? d : I), L);
 }

@@ -167,11 +167,24 @@ struct ExpertArgs {
   int64_t out_cs;
   int A;                    // T·k
   int calls;
+  // Intermediate rows in dispatch (sorted) order instead of assignment
+  // order: up writes act row p for sorted position p, down reads it there.
+  // Only the grouped GEMM honours it (the fused layer sets it for both
+  // products when both run on the GEMM).
+  int dispatch_order;
+  // Down on the grouped GEMM: K split into `parts` halves whose partial
+  // products go to out + part·A·N (the combine adds them). 0 or 1 = whole K.
+  int parts;
 };
 
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 // The grouped GEMM (gemm.hip) for many rows per expert.
 bool gemm_eligible(const ExpertArgs &ea);
+// Whether launch_expert runs these arguments on the grouped GEMM.
+bool expert_uses_gemm(const ExpertArgs &ea);
+// K parts the grouped GEMM uses for this down product (1 or 2): 2 when the
+// split evens out the last round of tiles over the CUs.
+int gemm_down_parts(const ExpertArgs &ea);
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 // Fills n floats with 0 (a kernel, not hipMemsetAsync, so a captured graph
 // replays it correctly).
@@ -179,6 +192,8 @@ int launch_zero(float *p, size_t n, hipStream_t s);
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s] per call.
 int launch_pack_quantw(const int8_t *ints, int E, int k, int n, int bits, uint32_t *words,
                        hipStream_t s);
-int launch_combine(const float *y, int64_t y_cs, const float *route, int64_t route_cs,
+// y holds `parts` partial products, part_cs floats apart (per call).
+int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, const float *route,
+                   int64_t route_cs,
                    const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
                    int64_t out_cs, int calls, hipStream_t s);

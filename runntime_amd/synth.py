@@ -28,7 +28,7 @@ class MoeConfig:
     I: int
     x_dtype: str  # "f32" | "f16"
     zipf: float = 0.0  # Zipf exponent of the router bias, 0 = none
-    hot_share: float = 0.20  # target share of the hottest expert under zipf
+    hot_share: float = 0.20  # share of tokens routed to the hottest expert under zipf
     tokens: int = 0  # decode configs: independent single-token calls timed
 
     @property
@@ -77,8 +77,13 @@ def _expert_weight(E, K, N, g, device, keep_q, bias_rand=False):
 
 def zipf_bias(cfg: MoeConfig, x: torch.Tensor, router_w: torch.Tensor, seed: int) -> torch.Tensor:
     """b_e = c·rank(e)^(−s) over a seeded permutation of the experts, with c
-    chosen (bisection, f64 on the CPU) so the hottest expert takes about
-    `hot_share` of the T·k assignments."""
+    chosen (bisection, f64 on the CPU) so that about `hot_share` of the
+    tokens route to the hottest expert.
+
+    The share is of tokens, not of the T·k assignments: a token picks an
+    expert at most once, so one expert can hold at most 1/k of the
+    assignments (12.5% at k = 8), and a search for 20% of them drives c to
+    its cap, where every token picks the same k experts."""
     g = _gen(seed + 7)
     perm = torch.randperm(cfg.E, generator=g)
     rank = torch.empty(cfg.E, dtype=torch.float64)
@@ -88,7 +93,7 @@ def zipf_bias(cfg: MoeConfig, x: torch.Tensor, router_w: torch.Tensor, seed: int
 
     def hottest(c):
         ids = torch.topk(logits + c * shape, cfg.k, dim=1).indices
-        return torch.bincount(ids.reshape(-1), minlength=cfg.E).max().item() / ids.numel()
+        return torch.bincount(ids.reshape(-1), minlength=cfg.E).max().item() / logits.shape[0]
 
     lo, hi = 0.0, 1.0
     while hottest(hi) < cfg.hot_share and hi < 1e4:
