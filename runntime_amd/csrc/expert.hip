@@ -478,6 +478,52 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
   out[call * out_cs + (int64_t)t * N + n] = acc;
 }
 
+// The same for N % 4 == 0, four columns per thread and every slot's loads
+// issued before the sums (the same order of operations per column).
+__global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, int64_t y_cs,
+                                                  int parts, int64_t part_cs,
+                                                  const float *__restrict__ route, int64_t route_cs,
+                                                  const float *__restrict__ residual, int64_t res_cs,
+                                                  int T, int N, int E, int k,
+                                                  float *__restrict__ out, int64_t out_cs) {
+  const int call = blockIdx.z;
+  const int t = blockIdx.x;
+  const int n = (blockIdx.y * 256 + threadIdx.x) * 4;
+  if (n >= N) return;
+  y += call * y_cs;
+  route += call * route_cs;
+  float4 acc = residual ? *(const float4 *)&residual[call * res_cs + (int64_t)t * N + n]
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 v[MAX_K];
+  float gate[MAX_K];
+#pragma unroll
+  for (int s = 0; s < MAX_K; s++) {
+    if (s >= k) break;
+    const int64_t asg = (int64_t)t * k + s;
+    const bool ok = route_expert(route, asg, k, E) >= 0;
+    gate[s] = ok ? route[(int64_t)t * 2 * k + k + s] : 0.f;
+    v[s] = ok ? *(const float4 *)&y[asg * N + n] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 1; q < parts; q++) {
+      if (!ok) break;
+      const float4 u = *(const float4 *)&y[q * part_cs + asg * N + n];
+      v[s].x += u.x;
+      v[s].y += u.y;
+      v[s].z += u.z;
+      v[s].w += u.w;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < MAX_K; s++) {
+    if (s >= k) break;
+    if (gate[s] == 0.f && route_expert(route, (int64_t)t * k + s, k, E) < 0) continue;
+    acc.x = fmaf(gate[s], v[s].x, acc.x);
+    acc.y = fmaf(gate[s], v[s].y, acc.y);
+    acc.z = fmaf(gate[s], v[s].z, acc.z);
+    acc.w = fmaf(gate[s], v[s].w, acc.w);
+  }
+  *(float4 *)&out[call * out_cs + (int64_t)t * N + n] = acc;
+}
+
 __global__ void k_zero(float *__restrict__ p, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -607,6 +653,14 @@ int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, con
   MOE_NONNULL(y);
   MOE_NONNULL(route);
   MOE_NONNULL(out);
+  auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  if (N % 4 == 0 && k <= MAX_K && a16(y) && a16(out) && (!residual || a16(residual)) &&
+      y_cs % 4 == 0 && part_cs % 4 == 0 && out_cs % 4 == 0 && res_cs % 4 == 0) {
+    dim3 grid(T, (N / 4 + 255) / 256, calls), block(256);
+    hipLaunchKernelGGL(k_combine4, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs,
+                       route, route_cs, residual, res_cs, T, N, E, k, out, out_cs);
+    return 0;
+  }
   dim3 grid(T, (N + 255) / 256, calls), block(256);
   hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs, route,
                      route_cs, residual, res_cs, T, N, E, k, out, out_cs);

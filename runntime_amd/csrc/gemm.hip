@@ -347,38 +347,56 @@ void k_expert_gemm(GemmArgs p) {
     asw[i] = SPLIT ? sw8(arow) : sw4(arow);
   }
 
-  auto compute = [&](int stage) {
+  // One step's fragments as read from LDS: raw weight tiles and A, per
+  // 16-k slice kk.
+  struct Frags {
+    u32x4 w[2][2];                 // [kk][tile]
+    u32x4 a[2][2][SPLIT ? 2 : 1];  // [kk][i][16-byte chunk]
+  };
+  auto read_frags = [&](Frags &F, int stage, int kk) {
     const uint8_t *st = lds + stage * STAGE;
+    const int t0 = 4 * h + 2 * kk;
+    F.w[kk][0] = *(const u32x4 *)(st + boff + ((t0 ^ bsw) * 16));
+    F.w[kk][1] = *(const u32x4 *)(st + boff + (((t0 + 1) ^ bsw) * 16));
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-      half8 bf[4];
-      const int t0 = 4 * h + 2 * kk;
-      const u32x4 d0 = *(const u32x4 *)(st + boff + ((t0 ^ bsw) * 16));
-      const u32x4 d1 = *(const u32x4 *)(st + boff + (((t0 + 1) ^ bsw) * 16));
-#pragma unroll
-      for (int c = 0; c < 4; c++) bf[c] = cvt_i8x8(d0[c], d1[c]);
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        half8 af[SPLIT ? 2 : 1];
-        if constexpr (SPLIT) {
-          const floatx4 v0 = *(const floatx4 *)(st + aoff[i] + ((t0 ^ asw[i]) * 16));
-          const floatx4 v1 = *(const floatx4 *)(st + aoff[i] + (((t0 + 1) ^ asw[i]) * 16));
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            const float x = j < 4 ? v0[j] : v1[j - 4];
-            const _Float16 xh = (_Float16)x;
-            af[0][j] = xh;
-            af[1][j] = (_Float16)(x - (float)xh);
-          }
-        } else {
-          af[0] = *(const half8 *)(st + aoff[i] + (((2 * h + kk) ^ asw[i]) * 16));
-        }
-#pragma unroll
-        for (int pl = 0; pl < (SPLIT ? 2 : 1); pl++)
-#pragma unroll
-          for (int c = 0; c < 4; c++)
-            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[pl], bf[c], acc[i][c], 0, 0, 0);
+    for (int i = 0; i < 2; i++) {
+      if constexpr (SPLIT) {
+        F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + ((t0 ^ asw[i]) * 16));
+        F.a[kk][i][1] = *(const u32x4 *)(st + aoff[i] + (((t0 + 1) ^ asw[i]) * 16));
+      } else {
+        F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + (((2 * h + kk) ^ asw[i]) * 16));
       }
+    }
+  };
+  // The MFMAs of one slice: column c outer, so converting column c + 1
+  // overlaps the MFMAs of column c.
+  auto mfma_slice = [&](const Frags &F, int kk) {
+    constexpr int PL = SPLIT ? 2 : 1;
+    half8 af[2][PL];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if constexpr (SPLIT) {
+        const floatx4 v0 = __builtin_bit_cast(floatx4, F.a[kk][i][0]);
+        const floatx4 v1 = __builtin_bit_cast(floatx4, F.a[kk][i][1]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float x = j < 4 ? v0[j] : v1[j - 4];
+          const _Float16 xh = (_Float16)x;
+          af[i][0][j] = xh;
+          af[i][PL - 1][j] = (_Float16)(x - (float)xh);
+        }
+      } else {
+        af[i][0] = __builtin_bit_cast(half8, F.a[kk][i][0]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const half8 bf = cvt_i8x8(F.w[kk][0][c], F.w[kk][1][c]);
+#pragma unroll
+      for (int pl = 0; pl < PL; pl++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+          acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][pl], bf, acc[i][c], 0, 0, 0);
     }
   };
 
@@ -459,16 +477,25 @@ void k_expert_gemm(GemmArgs p) {
     }
   };
 
-  // ---- the pipeline. Ring loads run STAGES − 1 steps ahead of the MFMAs,
+  // ---- the pipeline. Ring loads run STAGES steps ahead of the MFMAs,
   // across tile boundaries: the first steps of tile j + 1 load while tile j
-  // finishes and stores. The row map and constants of tile j + 1 load
-  // STAGES − 1 steps before its first ring load needs the row map. Each step
-  // waits (vmcnt) for this wavefront's ring loads of the step; the
-  // threshold counts what was issued after them: the ring loads of the next
-  // STAGES − 2 steps, plus the previous tile's epilogue stores in the first
-  // steps of a tile, plus the next tile's row map and constants while those
-  // are younger. The loop issues the same number of ring loads every step
-  // (past the last tile it re-reads the last step), so the counts hold.
+  // finishes and stores. Each step: the MFMAs of its first 16-k slice from
+  // registers; then (mid-step) wait for this wavefront's ring loads of the
+  // next step and for its own LDS reads, barrier (every wavefront's loads
+  // landed, every read of this step's slot done), load the step STAGES
+  // ahead into this step's slot, read the next step's first-slice
+  // fragments, run the second slice's MFMAs, and read the next step's
+  // second-slice fragments (their latency hides behind the next step's
+  // first slice). MFMAs issued before the barrier keep the matrix pipe busy
+  // while the wavefront waits there.
+  // The vmcnt threshold counts what was issued after the awaited loads: the
+  // ring loads of STAGES − 2 steps, plus the previous tile's epilogue stores
+  // in the first steps of a tile, plus the next tile's row map and constants
+  // while those are younger. The row map and constants of tile j + 1 load
+  // STAGES − 1 steps before the step whose wait covers them, where the next
+  // tile's load parameters are made (the step before its first ring load).
+  // Every step issues the same number of ring loads (past the last tile
+  // they re-read its last step), so the counts hold.
   Tile cur = tile_at(start), nxt = cur;
   issue_tile(cur, 0);
   WAIT_VMCNT(0);
@@ -476,9 +503,15 @@ void k_expert_gemm(GemmArgs p) {
   Params pc = make_params(cur, 0), pn = pc;
   if (ntiles > 1) nxt = tile_at(start + bx);
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; s++) issue(pc, cur.kb + s, s);
-  const int tile_step = ksteps - 2 * STAGES + 2;  // ≥ STAGES − 2 (checked on the host)
-  int stage = 0;
+  for (int s = 0; s < STAGES; s++) issue(pc, cur.kb + s, s);
+  WAIT_VMCNT((STAGES - 1) * LOADS);  // step 0
+  block_barrier();
+  Frags f;
+  read_frags(f, 0, 0);
+  read_frags(f, 0, 1);
+  const int tile_step = ksteps - 2 * STAGES;  // ≥ STAGES − 1 (checked on the host)
+  const int param_step = ksteps - STAGES - 1;
+  int stage = 0;  // slot of the step being computed
   for (int j = 0; j < ntiles; j++) {
     const bool has_next = j + 1 < ntiles;
     const int sel = j & 1;
@@ -492,20 +525,26 @@ void k_expert_gemm(GemmArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][c][r] = 0.f;
     for (int ks = 0; ks < ksteps; ks++) {
+      if (live) mfma_slice(f, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      // ---- mid-step
       if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(BASE_WAIT + STORES);
       else if (has_next && ks > tile_step && ks <= tile_step + STAGES - 2) WAIT_VMCNT(BASE_WAIT + TILE_LOADS);
       else WAIT_VMCNT(BASE_WAIT);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's LDS reads done
       block_barrier();
       if (has_next && ks == tile_step) issue_tile(nxt, sel ^ 1);
-      if (has_next && ks == ksteps - STAGES + 1) pn = make_params(nxt, sel ^ 1);
-      const int ahead = ks + STAGES - 1;
-      const int astage = stage == 0 ? STAGES - 1 : stage - 1;
-      if (ahead < ksteps) issue(pc, cur.kb + ahead, astage);
-      else if (has_next) issue(pn, nxt.kb + ahead - ksteps, astage);
-      else issue(pc, cur.kb + ksteps - 1, astage);
-      if (live) compute(stage);
-      __builtin_amdgcn_sched_barrier(0);
+      if (has_next && ks == param_step) pn = make_params(nxt, sel ^ 1);
+      const int ahead = ks + STAGES;
+      if (ahead < ksteps) issue(pc, cur.kb + ahead, stage);
+      else if (has_next) issue(pn, nxt.kb + ahead - ksteps, stage);
+      else issue(pc, cur.kb + ksteps - 1, stage);
       stage = stage + 1 == STAGES ? 0 : stage + 1;
+      read_frags(f, stage, 0);  // next step (the next tile's first after a tile's last)
+      __builtin_amdgcn_sched_barrier(0);
+      if (live) mfma_slice(f, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f, stage, 1);
     }
     epilogue(cur, wu, sel);
     if (has_next) {

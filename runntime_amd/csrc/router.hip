@@ -244,6 +244,67 @@ __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs r
   moe_dev::block_place(e, a, E, cursor, wc, perm);
 }
 
+// ---------------------------------------- chunk partials for many tokens
+
+// The same c_j as k_router_chunks, register-tiled: a block of 256 threads
+// takes TB tokens × EB experts of one chunk, each thread 4 tokens × 4
+// experts from two 16-byte LDS reads per k (x^T [64][TB], W [64][EB]).
+// For calls with more tokens than the one-block-per-call fused path.
+constexpr int RC_EB = 64;  // experts per block (E ≥ 64); TB = 64 tokens
+
+template <typename T, int EB>
+__global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
+  constexpr int EGN = EB / 4, TGN = 256 / EGN, TB = 4 * TGN;
+  __shared__ __align__(16) float xs[ROUTER_CHUNK * TB];  // [k][token]
+  __shared__ __align__(16) float ws[ROUTER_CHUNK * EB];  // [k][expert]
+  const int Tn = ra.T, d = ra.d, E = ra.E;
+  const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const int etiles = (E + EB - 1) / EB;
+  const int call = blockIdx.z / etiles;
+  const T *x = (const T *)ra.x + call * ra.x_cs;
+  const float *w = ra.w + call * ra.w_cs;
+  float *partial = ra.partial + call * ((int64_t)Tn * J * E);
+  const int t0 = blockIdx.x * TB;
+  const int j = blockIdx.y;
+  const int e0 = (blockIdx.z % etiles) * EB;
+  const int k0 = j * ROUTER_CHUNK;
+  const int len = min(ROUTER_CHUNK, d - k0);
+  const int tid = threadIdx.x;
+  for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
+    const int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK, t = t0 + tt;
+    xs[kk * TB + tt] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+  }
+  for (int i = tid; i < ROUTER_CHUNK * EB; i += 256) {
+    const int kk = i / EB, ee = i % EB, e = e0 + ee;
+    ws[i] = (kk < len && e < E) ? w[(int64_t)(k0 + kk) * E + e] : 0.f;
+  }
+  __syncthreads();
+  const int eg = tid % EGN, tg = tid / EGN;
+  float c[4][4] = {};
+  for (int kk = 0; kk < len; kk++) {
+    const float4 xv = *(const float4 *)&xs[kk * TB + 4 * tg];
+    const float4 wv = *(const float4 *)&ws[kk * EB + 4 * eg];
+    const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) c[a][q] = fmaf(xa[a], wa[q], c[a][q]);
+  }
+#pragma unroll
+  for (int a = 0; a < 4; a++) {
+    const int t = t0 + 4 * tg + a;
+    if (t >= Tn) break;
+    float *row = partial + ((int64_t)t * J + j) * E + e0 + 4 * eg;
+    if (e0 + 4 * eg + 3 < E && (E & 3) == 0) {
+      *(float4 *)row = make_float4(c[a][0], c[a][1], c[a][2], c[a][3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (e0 + 4 * eg + q < E) row[q] = c[a][q];
+    }
+  }
+}
+
 template <typename T>
 int topk_launch(const T *logits, int Tn, int E, int k, float *route, hipStream_t s) {
   dim3 grid((Tn + 3) / 4), block(256);
@@ -275,15 +336,31 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
   MOE_NONNULL(ra.partial);
   MOE_NONNULL(ra.route);
   if (ra.E > ROUTER_MAX_E) return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
-  const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-  const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
-  dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
-  if (ra.x_dtype == MOE_F16)
-    hipLaunchKernelGGL(k_router_chunks<_Float16>, grid, block, 0, s, ra);
-  else
-    hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, ra);
-  const int ni = (ra.E + WAVE - 1) / WAVE;
   const bool fuse = db && ra.T <= SMALL_T;
+  // Many tokens: the register-tiled chunk kernel (64 or 32 experts a block).
+  if (!fuse && ra.T > SMALL_T && ra.E >= 32) {
+    const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+    if (ra.E >= 64) {
+      const int tb = 4 * (256 / (64 / 4)), et = (ra.E + 63) / 64;
+      dim3 g((ra.T + tb - 1) / tb, J, et * ra.calls);
+      if (ra.x_dtype == MOE_F16) hipLaunchKernelGGL((k_router_chunks_tiled<_Float16, 64>), g, dim3(256), 0, s, ra);
+      else hipLaunchKernelGGL((k_router_chunks_tiled<float, 64>), g, dim3(256), 0, s, ra);
+    } else {
+      const int tb = 4 * (256 / (32 / 4)), et = (ra.E + 31) / 32;
+      dim3 g((ra.T + tb - 1) / tb, J, et * ra.calls);
+      if (ra.x_dtype == MOE_F16) hipLaunchKernelGGL((k_router_chunks_tiled<_Float16, 32>), g, dim3(256), 0, s, ra);
+      else hipLaunchKernelGGL((k_router_chunks_tiled<float, 32>), g, dim3(256), 0, s, ra);
+    }
+  } else {
+    const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+    const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
+    dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
+    if (ra.x_dtype == MOE_F16)
+      hipLaunchKernelGGL(k_router_chunks<_Float16>, grid, block, 0, s, ra);
+    else
+      hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, ra);
+  }
+  const int ni = (ra.E + WAVE - 1) / WAVE;
   if (dispatched) *dispatched = fuse;
   if (fuse) {
     MOE_NONNULL(db->offsets);
