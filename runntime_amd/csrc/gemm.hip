@@ -210,10 +210,13 @@ void k_expert_gemm(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform
-  // Wavefront w runs on SIMD w % 4, so each SIMD holds one wavefront of
-  // each row half: a tile of at most 64 rows, whose second half skips its
-  // MFMAs, leaves every SIMD one busy wavefront instead of idling two.
-  const int wm = wave >> 2, wn = wave & 3;
+  // Wavefront w runs on SIMD w % 4. Each SIMD holds one wavefront of each
+  // row half, the second with the unit group mirrored by 2 (SIMD s: unit
+  // groups s and s ^ 2). A tile of at most 64 rows (second row half idle)
+  // or of at most 32 units per source (unit groups 2 and 3 idle, as in the
+  // last N-tile of I = 1408) then leaves every SIMD one busy wavefront
+  // instead of idling two SIMDs.
+  const int wm = wave >> 2, wn = wm ? (wave & 3) ^ 2 : wave & 3;
   const int lm = lane & 31, h = lane >> 5;
   const int N4 = p.N / 4;
   const int ksteps = p.kpart;  // steps per tile
