@@ -478,13 +478,16 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
   out[call * out_cs + (int64_t)t * N + n] = acc;
 }
 
-// The same for N % 4 == 0, four columns per thread and every slot's loads
-// issued before the sums (the same order of operations per column).
+// The same for N % 4 == 0: four columns per thread, the slot count a
+// template parameter so every slot's loads are in flight together (a
+// runtime count leaves the slot array in scratch memory, one load at a
+// time); the same order of operations per column.
+template <int KK>
 __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, int64_t y_cs,
                                                   int parts, int64_t part_cs,
                                                   const float *__restrict__ route, int64_t route_cs,
                                                   const float *__restrict__ residual, int64_t res_cs,
-                                                  int T, int N, int E, int k,
+                                                  int T, int N, int E,
                                                   float *__restrict__ out, int64_t out_cs) {
   const int call = blockIdx.z;
   const int t = blockIdx.x;
@@ -492,20 +495,23 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, i
   if (n >= N) return;
   y += call * y_cs;
   route += call * route_cs;
+  float4 v[KK];
+  bool ok[KK];
+  float gate[KK];
+#pragma unroll
+  for (int s = 0; s < KK; s++) {
+    const int64_t asg = (int64_t)t * KK + s;
+    ok[s] = route_expert(route, asg, KK, E) >= 0;
+    gate[s] = route[(int64_t)t * 2 * KK + KK + s];
+    v[s] = *(const float4 *)&y[asg * N + n];
+  }
+  // The residual after the slot loads, so they all wait together.
   float4 acc = residual ? *(const float4 *)&residual[call * res_cs + (int64_t)t * N + n]
                         : make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 v[MAX_K];
-  float gate[MAX_K];
+  for (int q = 1; q < parts; q++) {
 #pragma unroll
-  for (int s = 0; s < MAX_K; s++) {
-    if (s >= k) break;
-    const int64_t asg = (int64_t)t * k + s;
-    const bool ok = route_expert(route, asg, k, E) >= 0;
-    gate[s] = ok ? route[(int64_t)t * 2 * k + k + s] : 0.f;
-    v[s] = ok ? *(const float4 *)&y[asg * N + n] : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int q = 1; q < parts; q++) {
-      if (!ok) break;
-      const float4 u = *(const float4 *)&y[q * part_cs + asg * N + n];
+    for (int s = 0; s < KK; s++) {
+      const float4 u = *(const float4 *)&y[q * part_cs + ((int64_t)t * KK + s) * N + n];
       v[s].x += u.x;
       v[s].y += u.y;
       v[s].z += u.z;
@@ -513,9 +519,8 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, i
     }
   }
 #pragma unroll
-  for (int s = 0; s < MAX_K; s++) {
-    if (s >= k) break;
-    if (gate[s] == 0.f && route_expert(route, (int64_t)t * k + s, k, E) < 0) continue;
+  for (int s = 0; s < KK; s++) {
+    if (!ok[s]) continue;
     acc.x = fmaf(gate[s], v[s].x, acc.x);
     acc.y = fmaf(gate[s], v[s].y, acc.y);
     acc.z = fmaf(gate[s], v[s].z, acc.z);
@@ -654,12 +659,20 @@ int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, con
   MOE_NONNULL(route);
   MOE_NONNULL(out);
   auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
-  if (N % 4 == 0 && k <= MAX_K && a16(y) && a16(out) && (!residual || a16(residual)) &&
+  if (N % 4 == 0 && (k <= 8 || k == 16) && a16(y) && a16(out) && (!residual || a16(residual)) &&
       y_cs % 4 == 0 && part_cs % 4 == 0 && out_cs % 4 == 0 && res_cs % 4 == 0) {
     dim3 grid(T, (N / 4 + 255) / 256, calls), block(256);
-    hipLaunchKernelGGL(k_combine4, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs,
-                       route, route_cs, residual, res_cs, T, N, E, k, out, out_cs);
+    const int pp = parts < 1 ? 1 : parts;
+#define COMBINE4(KK_)                                                                        \
+  case KK_:                                                                                  \
+    hipLaunchKernelGGL(k_combine4<KK_>, grid, block, 0, s, y, y_cs, pp, part_cs, route,      \
+                       route_cs, residual, res_cs, T, N, E, out, out_cs);                    \
     return 0;
+    switch (k) {
+      COMBINE4(1) COMBINE4(2) COMBINE4(3) COMBINE4(4) COMBINE4(5) COMBINE4(6) COMBINE4(7)
+      COMBINE4(8) COMBINE4(16)
+    }
+#undef COMBINE4
   }
   dim3 grid(T, (N + 255) / 256, calls), block(256);
   hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs, route,
