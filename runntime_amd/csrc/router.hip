@@ -22,6 +22,7 @@
 namespace {
 
 constexpr float NEG_START = -3.4e38f;
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 constexpr int WAVE = 64;
 
 __device__ __forceinline__ float load_as_f32(const float *p, int64_t i) { return p[i]; }
@@ -270,13 +271,45 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
   const int tid = threadIdx.x;
-  for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
-    const int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK, t = t0 + tt;
-    xs[kk * TB + tt] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
-  }
-  for (int i = tid; i < ROUTER_CHUNK * EB; i += 256) {
-    const int kk = i / EB, ee = i % EB, e = e0 + ee;
-    ws[i] = (kk < len && e < E) ? w[(int64_t)(k0 + kk) * E + e] : 0.f;
+  // Staging in 16-byte loads where the chunk is whole and aligned: x as
+  // 8-element runs of a token's row (stored transposed), W as 4-expert runs.
+  const bool vec = len == ROUTER_CHUNK && (d & 7) == 0 && (E & 3) == 0 && e0 + EB <= E;
+  if (vec) {
+    constexpr int XR = ROUTER_CHUNK / 8;  // runs per token row
+    for (int i = tid; i < TB * XR; i += 256) {
+      const int tt = i / XR, kk = (i % XR) * 8, t = t0 + tt;
+      float v[8];
+      if (t < Tn) {
+        if constexpr (sizeof(T) == 2) {
+          const half8v h = *(const half8v *)((const _Float16 *)x + (int64_t)t * d + k0 + kk);
+#pragma unroll
+          for (int q = 0; q < 8; q++) v[q] = (float)h[q];
+        } else {
+          const float4 a = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk);
+          const float4 b = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk + 4);
+          v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+          v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; q++) xs[(kk + q) * TB + tt] = v[q];
+    }
+    for (int i = tid; i < ROUTER_CHUNK * EB / 4; i += 256) {
+      const int kk = i / (EB / 4), ee = (i % (EB / 4)) * 4;
+      *(float4 *)&ws[kk * EB + ee] = *(const float4 *)&w[(int64_t)(k0 + kk) * E + e0 + ee];
+    }
+  } else {
+    for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
+      const int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK, t = t0 + tt;
+      xs[kk * TB + tt] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+    }
+    for (int i = tid; i < ROUTER_CHUNK * EB; i += 256) {
+      const int kk = i / EB, ee = i % EB, e = e0 + ee;
+      ws[i] = (kk < len && e < E) ? w[(int64_t)(k0 + kk) * E + e] : 0.f;
+    }
   }
   __syncthreads();
   const int eg = tid % EGN, tg = tid / EGN;
