@@ -153,8 +153,8 @@ MFMA_SHAPES = [(3, 64, 72, 5, 64), (40, 96, 136, 6, 32), (100, 100, 80, 3, 100),
                (17, 2048, 1408, 4, 2048), (64, 512, 1024, 8, 512), (9, 640, 640, 16, 64)]
 
 
-def _check_up(T, K, N, E, g, bits, k=4, xdtype="f32", tol="ref"):
-    route = route_for(T, E, k)
+def _check_up(T, K, N, E, g, bits, k=4, xdtype="f32", tol="ref", route=None):
+    route = route_for(T, E, k) if route is None else route
     glu, glu_h = weight_pair(E, K, N, bits, g, 10)
     lin, lin_h = weight_pair(E, K, N, bits, g, 20)
     x = (ref.lcg_f32(T * K, 1) * 4).reshape(T, K)
@@ -168,8 +168,8 @@ def _check_up(T, K, N, E, g, bits, k=4, xdtype="f32", tol="ref"):
     assert_close(got, want, what="moeUp")
 
 
-def _check_down(T, K, N, E, g, bits, k=4):
-    route = route_for(T, E, k)
+def _check_down(T, K, N, E, g, bits, k=4, route=None):
+    route = route_for(T, E, k) if route is None else route
     down, down_h = weight_pair(E, K, N, bits, g, 30)
     act = ref.lcg_f32(T * k * K, 1).reshape(T * k, K)
     res = ref.lcg_f32(T * N, 4).reshape(T, N)
@@ -216,26 +216,58 @@ def test_moe_down_mfma(shape, k):
     _check_down(T, K, N, E, g, 8, k=k)
 
 
-# Rows per expert ≥ 64 on average: these take the grouped GEMM (128×128
-# tiles). Ragged last M-tiles, grids that are not a multiple of 8 blocks,
-# K not a multiple of 128.
+# Rows per expert ≥ 64 on average: shapes for the grouped GEMM path. The
+# first list keeps K short, below the GEMM's load ring (≥ 18 steps of 32 for
+# f16 input, ≥ 12 for f32), so most of it runs the skinny kernel on many rows.
 GEMM_SHAPES = [(300, 128, 256, 4, 128), (260, 192, 128, 3, 192), (1000, 256, 384, 8, 256),
                (2048, 512, 640, 16, 512)]
+# These take the grouped GEMM: ragged last M-tiles, an N-tile with only part
+# of its units (N not a multiple of 256 / 512, and I = 1408's half tile),
+# the shortest K the ring takes.
+GEMM_UP_SHAPES = [(300, 640, 264, 4, 640), (1000, 768, 1408, 8, 768), (2048, 576, 640, 16, 576),
+                  (600, 384, 136, 3, 384)]
+# Down: the last two split K into two partial products (few tiles for the
+# CUs), added by the combine.
+GEMM_DOWN_SHAPES = [(300, 384, 520, 4, 384), (1000, 1408, 2048, 8, 1408), (512, 5632, 256, 4, 5632)]
 
 
 @pytest.mark.parametrize("xdtype", ["f32", "f16"])
-@pytest.mark.parametrize("shape", GEMM_SHAPES)
+@pytest.mark.parametrize("shape", GEMM_SHAPES + GEMM_UP_SHAPES)
 def test_moe_up_grouped_gemm(xdtype, shape):
     T, K, N, E, g = shape
     say(f"moeUp gemm {xdtype} {shape}")
     _check_up(T, K, N, E, g, 8, k=2, xdtype=xdtype)
 
 
-@pytest.mark.parametrize("shape", GEMM_SHAPES)
+@pytest.mark.parametrize("shape", GEMM_SHAPES + GEMM_DOWN_SHAPES)
 def test_moe_down_grouped_gemm(shape):
     T, K, N, E, g = shape
     say(f"moeDown gemm {shape}")
     _check_down(T, K, N, E, g, 8, k=2)
+
+
+def _skewed_route(T, k=2):
+    """Slot 0 → experts 0-2, slot 1 → experts 5-6 of 8: experts 3, 4 and 7
+    get no rows, the others hundreds (uneven)."""
+    route = np.zeros((T, 2 * k), np.float32)
+    for t in range(T):
+        route[t, 0] = t % 3
+        route[t, 1] = 5 + (t % 7 == 0)
+        route[t, 2:] = (0.625, 0.375)
+    return route
+
+
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+def test_moe_up_gemm_empty_experts(xdtype):
+    say(f"moeUp gemm empty experts {xdtype}")
+    T = 1024
+    _check_up(T, 640, 264, 8, 640, 8, k=2, xdtype=xdtype, route=_skewed_route(T))
+
+
+def test_moe_down_gemm_empty_experts():
+    say("moeDown gemm empty experts")
+    T = 1024
+    _check_down(T, 384, 520, 8, 384, 8, k=2, route=_skewed_route(T))
 
 
 def test_moe_up_past_65535_rows():
