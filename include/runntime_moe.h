@@ -16,6 +16,9 @@
  *                                                  kernel src/core/kernels/matmul/moeQuantW.ts:188-237
  *   moe_layer        the quantized branch of EagerMoeMlp.forward after rmsNorm:
  *                    topk(router) → moeUp → moeDown  src/zoo/privacy-filter/moeMlp.ts:82-121
+ *   moe_weights_upload / _view / _dispose / _release
+ *                    a QuantExpertWeight's buffers uploaded and owned by the
+ *                    library (Parameter, src/core/nn/module.ts:20-65)
  *   moe_ctx_* / moe_sync / moe_last_error
  *                    the executor contract the ops run under: one queue per
  *                    context, errors as codes (src/core/graph/evalCore.ts:14-31,
@@ -191,6 +194,31 @@ MOE_API int moe_dispatch(moe_ctx *ctx, const float *route, int T, int E, int k, 
  * be multiples of 4; bits 8 or 4. */
 MOE_API int moe_pack_quantw(moe_ctx *ctx, const int8_t *ints, int E, int k, int n, int bits,
                             uint32_t *words);
+
+/* An expert weight owned by the library: device copies of one
+ * QuantExpertWeight's w, scales and bias — the weight-load step the
+ * reference does through a Parameter, which owns its GPU buffer
+ * (src/core/nn/module.ts:20-65; weights uploaded with upload(),
+ * test/gpu.ts:73-83, packed by packQuantW, src/core/weights/quantPack.ts).
+ * host: quantW words (E·K·N·bits/32 u32) when raw_int8 is 0, else int8
+ * [E][N][K] (each expert output-first, one value per byte) packed on the
+ * device; scales f32 [E·K/groupSize, N]; bias f32 [E, N] or NULL. All host
+ * pointers; the call returns once they may be freed. An empty shape is
+ * INVALID_ARGUMENT, as the reference's upload of an empty tensor
+ * (test/core/kernels/matmul/moeQuantW.gpu.test.ts:167-171). */
+typedef struct moe_weights moe_weights;
+MOE_API int moe_weights_upload(moe_ctx *ctx, const void *host, int raw_int8, const float *scales,
+                               const float *bias, int E, int K, int N, int bits, int group_size,
+                               moe_weights **out);
+/* The device pointers of an uploaded weight, for moe_up / moe_down /
+ * moe_layer. RESOURCE_DISPOSED after moe_weights_dispose (the reference's
+ * use of a disposed Value). */
+MOE_API int moe_weights_view(const moe_weights *h, moe_expert_weight *view);
+/* Frees the device buffers (Parameter.dispose()); the handle stays valid
+ * and reports RESOURCE_DISPOSED. Waits for work already enqueued. */
+MOE_API int moe_weights_dispose(moe_weights *h);
+/* Disposes if needed and frees the handle itself. */
+MOE_API int moe_weights_release(moe_weights *h);
 
 #ifdef __cplusplus
 }

@@ -10,11 +10,12 @@ include/runntime_moe.h for its C ABI.
 from .errors import RUNNTIME_ERROR_CODES, RunntimeError, is_runntime_error
 from .quantw import (QuantExpertWeight, QuantW, pack_expert_weights, pack_expert_weights_torch,
                      pack_quant_w)
-from .core import dispatch, moe_layer, pack_quant_w_device, moe_layer_batched, moeDown, moeUp, router_topk, topk
+from .core import (UploadedExpertWeight, dispatch, moe_layer, moe_layer_batched, moeDown, moeUp,
+                   pack_quant_w_device, router_topk, topk, upload_expert_weight)
 
 __all__ = [
     "RUNNTIME_ERROR_CODES", "RunntimeError", "is_runntime_error", "QuantExpertWeight", "QuantW",
     "pack_expert_weights", "pack_expert_weights_torch", "pack_quant_w", "dispatch", "moe_layer",
     "moe_layer_batched", "pack_quant_w_device",
-    "moeDown", "moeUp", "router_topk", "topk",
+    "moeDown", "moeUp", "router_topk", "topk", "UploadedExpertWeight", "upload_expert_weight",
 ]

@@ -20,6 +20,7 @@ EXPORTED = (
     "moe_ctx_reserve", "moe_ctx_destroy", "moe_sync", "moe_topk", "moe_router_topk",
     "moe_up", "moe_down", "moe_layer", "moe_dispatch", "moe_prof_enable", "moe_prof_read",
     "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
+    "moe_weights_upload", "moe_weights_view", "moe_weights_dispose", "moe_weights_release",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine")
 
@@ -74,6 +75,10 @@ def load() -> ctypes.CDLL:
                                    I, I, I, I, I, I, I, P, P], I),
             "moe_ctx_reserve_batched": ([P, I, I, I, I, I, I], I),
             "moe_prof_read": ([P, I, P, P], I),
+            "moe_weights_upload": ([P, P, I, P, P, I, I, I, I, I, ctypes.POINTER(P)], I),
+            "moe_weights_view": ([P, W], I),
+            "moe_weights_dispose": ([P], I),
+            "moe_weights_release": ([P], I),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)

@@ -345,3 +345,50 @@ def moe_layer_batched(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantE
         _ptr(router_b), ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn), _ptr(residual), t, d,
         i, e, k, bits, gu, gd, route.data_ptr(), out.data_ptr()))
     return out, route
+
+
+# ------------------------------------------------------------ weight upload
+
+
+class UploadedExpertWeight:
+    """A QuantExpertWeight whose device buffers the library owns
+    (moe_weights_upload): the reference's Parameter, which owns its GPU
+    buffer and frees it on dispose() (src/core/nn/module.ts:20-65). `view()`
+    gives the device pointers the C ABI takes; after `dispose()` it raises
+    RESOURCE_DISPOSED."""
+
+    def __init__(self, handle: int, E: int, K: int, N: int, bits: int, group_size: int):
+        self.handle, self.E, self.K, self.N = handle, E, K, N
+        self.bits, self.group_size = bits, group_size
+
+    def view(self) -> _lib.ExpertWeightC:
+        v = _lib.ExpertWeightC()
+        _lib.check(_lib.load().moe_weights_view(self.handle, ctypes.byref(v)))
+        return v
+
+    def dispose(self) -> None:
+        _lib.check(_lib.load().moe_weights_dispose(self.handle))
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _lib.load().moe_weights_release(self.handle)
+            self.handle = None
+
+
+def upload_expert_weight(host_w, scales, bias, E: int, K: int, N: int, bits: int,
+                         group_size: int, raw_int8: bool = False,
+                         device: int = 0) -> UploadedExpertWeight:
+    """Uploads host buffers (numpy): quantW words (uint32, E·K·N·bits/32),
+    or int8 [E][N][K] with raw_int8 (packed on the device as packQuantW);
+    scales f32 [E·K/groupSize, N]; bias f32 [E, N] or None."""
+    import numpy as np
+    hw = np.ascontiguousarray(host_w)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    bs = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    ctx = _lib.context(device, 0)
+    out = ctypes.c_void_p()
+    _lib.check(_lib.load().moe_weights_upload(
+        ctx, hw.ctypes.data if hw.size else None, 1 if raw_int8 else 0,
+        sc.ctypes.data if sc.size else None, None if bs is None else bs.ctypes.data,
+        E, K, N, bits, group_size, ctypes.byref(out)))
+    return UploadedExpertWeight(out.value, E, K, N, bits, group_size)

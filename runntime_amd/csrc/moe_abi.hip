@@ -562,3 +562,119 @@ extern "C" int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, in
   return plan_ws(ctx, calls, T, k, E, (size_t)T * 2 * k, router_partial_floats(T, d, E),
                  (size_t)T * k * I, (size_t)2 * T * k * (d > I ? d : I), L);
 }
+
+// ------------------------------------------------------------ weight upload
+
+// An expert weight owned by the library (QuantExpertWeight's three device
+// buffers). After moe_weights_dispose the handle stays valid and reports
+// RESOURCE_DISPOSED until moe_weights_release frees it.
+struct moe_weights {
+  int device = 0;
+  bool disposed = false;
+  uint32_t *w = nullptr;
+  float *scales = nullptr;
+  float *bias = nullptr;
+  int E = 0, K = 0, N = 0, bits = 0, g = 0;
+};
+
+static void weights_free(moe_weights *h) {
+  if (h->w) (void)hipFree(h->w);
+  if (h->scales) (void)hipFree(h->scales);
+  if (h->bias) (void)hipFree(h->bias);
+  h->w = nullptr;
+  h->scales = nullptr;
+  h->bias = nullptr;
+}
+
+extern "C" int moe_weights_upload(moe_ctx *ctx, const void *host, int raw_int8,
+                                  const float *scales, const float *bias, int E, int K, int N,
+                                  int bits, int group_size, moe_weights **out) {
+  int rc = check_ctx(ctx, "upload");
+  if (rc) return rc;
+  REQUIRE(out, "upload: NULL handle");
+  *out = nullptr;
+  REQUIRE((long)E * K * N > 0 && E > 0 && K > 0 && N > 0, "upload: the shape has no elements");
+  REQUIRE(host && scales, "upload: NULL tensor");
+  REQUIRE(bits == 8 || bits == 4, "upload: bits must be 8 or 4, got " + S(bits));
+  REQUIRE(K % 4 == 0 && N % 4 == 0,
+          "upload: K " + S(K) + " and N " + S(N) + " must be multiples of 4");
+  REQUIRE(group_size > 0 && group_size % 4 == 0 && K % group_size == 0,
+          "upload: groupSize " + S(group_size) + " must be a multiple of 4 that divides K " + S(K));
+  REQUIRE(E <= 1024, "upload: expert count must be in 1..1024, got " + S(E));
+  moe_weights *h = new moe_weights;
+  h->device = ctx->device;
+  h->E = E;
+  h->K = K;
+  h->N = N;
+  h->bits = bits;
+  h->g = group_size;
+  const size_t words = (size_t)E * K * N * bits / 32;
+  const size_t n_scales = (size_t)E * K / group_size * N;
+  const size_t n_bias = (size_t)E * N;
+  int8_t *tmp = nullptr;
+  auto fail = [&](hipError_t e, const char *what) {
+    if (tmp) (void)hipFree(tmp);
+    weights_free(h);
+    delete h;
+    return moe_fail(MOE_EXECUTION_FAILED, std::string("upload: ") + what + ": " + hipGetErrorString(e));
+  };
+  hipError_t e;
+  if ((e = hipMalloc(&h->w, words * 4)) != hipSuccess) return fail(e, "hipMalloc");
+  if ((e = hipMalloc(&h->scales, n_scales * 4)) != hipSuccess) return fail(e, "hipMalloc");
+  if (bias && (e = hipMalloc(&h->bias, n_bias * 4)) != hipSuccess) return fail(e, "hipMalloc");
+  hipStream_t s = ctx->stream;
+  if (raw_int8) {
+    // int8 [E][N][K] (output-first per expert, one value per byte) packed
+    // on the device, as packQuantW per expert, experts concatenated.
+    const size_t n_ints = (size_t)E * K * N;
+    if ((e = hipMalloc(&tmp, n_ints)) != hipSuccess) return fail(e, "hipMalloc");
+    if ((e = hipMemcpyAsync(tmp, host, n_ints, hipMemcpyHostToDevice, s)) != hipSuccess)
+      return fail(e, "hipMemcpy");
+    if ((rc = launch_pack_quantw(tmp, E, K, N, bits, h->w, s))) {
+      (void)hipStreamSynchronize(s);
+      (void)hipFree(tmp);
+      weights_free(h);
+      delete h;
+      return rc;
+    }
+  } else if ((e = hipMemcpyAsync(h->w, host, words * 4, hipMemcpyHostToDevice, s)) != hipSuccess) {
+    return fail(e, "hipMemcpy");
+  }
+  if ((e = hipMemcpyAsync(h->scales, scales, n_scales * 4, hipMemcpyHostToDevice, s)) != hipSuccess)
+    return fail(e, "hipMemcpy");
+  if (bias && (e = hipMemcpyAsync(h->bias, bias, n_bias * 4, hipMemcpyHostToDevice, s)) != hipSuccess)
+    return fail(e, "hipMemcpy");
+  // The host buffers may be released once this returns.
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail(e, "hipStreamSynchronize");
+  if (tmp) (void)hipFree(tmp);
+  *out = h;
+  return MOE_OK;
+}
+
+extern "C" int moe_weights_view(const moe_weights *h, moe_expert_weight *view) {
+  if (!h) return moe_fail(MOE_NOT_INITIALIZED, "weights: handle is NULL");
+  if (h->disposed) return moe_fail(MOE_RESOURCE_DISPOSED, "weights: used after dispose");
+  REQUIRE(view, "weights: NULL view");
+  view->w = h->w;
+  view->scales = h->scales;
+  view->bias = h->bias;
+  return MOE_OK;
+}
+
+extern "C" int moe_weights_dispose(moe_weights *h) {
+  if (!h) return moe_fail(MOE_NOT_INITIALIZED, "weights: handle is NULL");
+  if (h->disposed) return MOE_OK;
+  (void)hipSetDevice(h->device);
+  // Work already enqueued on these buffers must finish before they go.
+  MOE_HIP_CHECK(hipDeviceSynchronize());
+  weights_free(h);
+  h->disposed = true;
+  return MOE_OK;
+}
+
+extern "C" int moe_weights_release(moe_weights *h) {
+  if (!h) return MOE_OK;
+  int rc = moe_weights_dispose(h);
+  delete h;
+  return rc;
+}

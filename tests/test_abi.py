@@ -167,3 +167,12 @@ def test_pack_quant_w_device_rejects_host_or_wrong_dtype():
         rt.pack_quant_w_device(torch.zeros((2, 8, 8), dtype=torch.int8))
     with pytest.raises(ValueError, match="packQuantW"):
         rt.pack_quant_w_device(torch.zeros((2, 8, 8), dtype=torch.int32))
+
+
+def test_weights_null_handle_paths():
+    """moe_weights_view on no handle is NOT_INITIALIZED; releasing none is a no-op."""
+    lib = _lib.load()
+    v = _lib.ExpertWeightC()
+    assert lib.moe_weights_view(None, ctypes.byref(v)) == 3
+    assert b"handle is NULL" in lib.moe_last_error()
+    assert lib.moe_weights_release(None) == 0

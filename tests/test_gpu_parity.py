@@ -445,3 +445,52 @@ def test_pack_quant_w_device_matches_packquantw(bits, E, k, n):
     got = host(rt.pack_quant_w_device(gpu(ints), bits).words).view(np.uint32)
     want = np.concatenate([ref.pack_nk(ints[e], k, n, bits) for e in range(E)])
     np.testing.assert_array_equal(got, want)
+
+
+# ----------------------------------------------------------- weight upload
+
+
+@pytest.mark.parametrize("raw", [False, True])
+def test_uploaded_weights_match_device_tensors(raw):
+    """moeUp through the C ABI with moe_weights_upload's buffers equals moeUp
+    with the same weights as torch tensors; raw int8 [E][N][K] is packed on
+    the device (packQuantW)."""
+    import ctypes
+    from runntime_amd import _lib
+    say(f"upload raw={raw}")
+    T, K, N, E, g, k = 40, 96, 136, 6, 32, 4
+    glu, (gw, gs, gb) = weight_pair(E, K, N, 8, g, 10)
+    lin, (lw, ls, lb) = weight_pair(E, K, N, 8, g, 20)
+    if raw:
+        qg = np.stack([ref.unpack(gw, E, K, N, 8)[e].T for e in range(E)])  # [E][N][K]
+        ql = np.stack([ref.unpack(lw, E, K, N, 8)[e].T for e in range(E)])
+        ug = rt.upload_expert_weight(qg.astype(np.int8), gs, gb, E, K, N, 8, g, raw_int8=True)
+        ul = rt.upload_expert_weight(ql.astype(np.int8), ls, lb, E, K, N, 8, g, raw_int8=True)
+    else:
+        ug = rt.upload_expert_weight(gw, gs, gb, E, K, N, 8, g)
+        ul = rt.upload_expert_weight(lw, ls, lb, E, K, N, 8, g)
+    route = route_for(T, E, k)
+    x = (ref.lcg_f32(T * K, 1) * 4).reshape(T, K)
+    xt, rt_route = gpu(x), gpu(route)
+    want = host(rt.moeUp(xt, rt_route, glu, lin, {"bits": 8, "groupSize": g}))
+    act = torch.empty((T * k, N), device=DEV)
+    lib = _lib.load()
+    vg, vl = ug.view(), ul.view()
+    ctx = _lib.context(0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(lib.moe_up(ctx, xt.data_ptr(), _lib.MOE_F32, rt_route.data_ptr(), ctypes.byref(vg),
+                          ctypes.byref(vl), T, K, N, E, k, 8, g, act.data_ptr()))
+    assert np.array_equal(host(act), want)
+    ug.dispose()
+    with pytest.raises(rt.RunntimeError) as ei:
+        ug.view()
+    assert ei.value.code == "RESOURCE_DISPOSED"
+
+
+def test_upload_rejects_an_empty_shape():
+    """moeQuantW.gpu.test.ts:167-171: an empty upload is INVALID_ARGUMENT."""
+    say("upload empty")
+    with pytest.raises(rt.RunntimeError) as ei:
+        rt.upload_expert_weight(np.zeros(0, np.uint32), np.zeros(0, np.float32), None,
+                                0, 4, 4, 8, 4)
+    assert ei.value.code == "INVALID_ARGUMENT"
+    assert "no elements" in str(ei.value)
