@@ -109,34 +109,39 @@ __host__ __device__ __forceinline__ int a_stage_rows(int K, bool split) {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
-// Lane group kq of a 32-wide K step holds k ∈ {4kq..4kq+3} ∪ {16+4kq..}: the
-// same k as the lane's B tiles (8·step + kq and 8·step + 4 + kq).
+// Lane group kq of a 32-wide K step holds k = 8kq .. 8kq+7 of its row: the
+// same k as the lane's B tiles (2kq and 2kq + 1 of the step).
 __device__ __forceinline__ half8 a_frag(const _Float16 *plane, int kp, int row, int step, int kq) {
-  const _Float16 *p = plane + row * kp + step * 32 + 4 * kq;
-  half4 lo = *(const half4 *)p;
-  half4 hi = *(const half4 *)(p + 16);
-  half8 r;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    r[j] = lo[j];
-    r[4 + j] = hi[j];
-  }
-  return r;
+  return *(const half8 *)(plane + row * kp + step * 32 + 8 * kq);
 }
-
-// Weight tiles of one K step of one wavefront.
-struct WStep {
-  uint4 t0, t1;
-};
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// Weight tiles are read with plain loads: the 4 lanes of a unit read half
-// of a 128-byte line per instruction and the next instruction reads the
-// other half, which then comes from L2. (Nontemporal loads refetch it: on
-// MI355X they made this kernel ~25% slower, though they stream whole lines
-// faster than plain loads.)
-__device__ __forceinline__ uint4 load_stream(const uint4 *p) { return *p; }
+// Weight tiles of one K step of one wavefront, as loaded: t0 from the
+// wavefront's units 0-7, t1 from units 8-15 (see the load mapping below).
+struct WStep {
+  u32x4 t0, t1;
+};
+
+// Weight loads. A step's two load instructions each cover whole 128-byte
+// lines (8 units × the step's 8 tiles), so a nontemporal load fetches every
+// line once; the lanes then trade tiles (row_ror:8) into the MFMA layout.
+// Nontemporal loads stream from HBM at ~7.1 TB/s on MI355X against ~6.3 TB/s
+// for plain loads (same access pattern, measured). They are buffer loads
+// with no branch around them: an offset past the buffer reads zeros, so a
+// tile past K or a unit past N costs no divergent code, and the compiler's
+// wait counts stay exact (a load under a branch makes it wait for every
+// load in flight at the join, which empties the pipeline).
+constexpr uint32_t OOB = 0x80000000u;
+constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer, 32-bit data format
+__device__ __forceinline__ u32x4 load_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2 /* nt */));
+}
+
+// Lane L of a 16-lane row receives the value of lane L ^ 8 (DPP row_ror:8).
+__device__ __forceinline__ uint32_t swap8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, false);
+}
 
 // k_expert_skinny: one block = one active expert × NW·(column groups per
 // wavefront) groups of 64 output columns (16 quantW units each). The
@@ -199,7 +204,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
   floatx4 *park = (floatx4 *)(smem + (size_t)RC * kp * 2 * planes) +
                   (PAIRED ? (wave >> 1) : wave) * 4 * WAVE;
 
-  const uint4 *wt[NS];
+  // Loaded units: instruction 0 takes unit 16·cg + (lane & 7), instruction 1
+  // unit 16·cg + 8 + (lane & 7); tile (lane >> 3) of the step, ^ 1 for
+  // instruction 1. After the row_ror:8 trade every lane holds tiles 2kq and
+  // 2kq + 1 of its own unit 16·cg + (lane & 15).
+  __amdgpu_buffer_rsrc_t wr[NS];
+  uint32_t wl[NS][2];  // byte offset of the lane's unit in the expert's slab, or OOB
   const float *sc[NS];
   floatx4 sone[NS], bias[NS];
 #pragma unroll
@@ -209,7 +219,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     sc[j] = second ? p.s1 + call * p.s1_cs : p.s0 + call * p.s0_cs;
     const float *b = second ? (p.b1 ? p.b1 + call * p.b1_cs : nullptr)
                             : (p.b0 ? p.b0 + call * p.b0_cs : nullptr);
-    wt[j] = (const uint4 *)w + ((int64_t)e * N4 + (uok[j] ? useg[j] : 0)) * K4;
+    const uint32_t slab = (uint32_t)p.K * (uint32_t)p.N * (uint32_t)p.bits / 8u;
+    wr[j] = __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)w + (int64_t)e * slab), 0,
+                                              (int)slab, BUF_DWORD3);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+      const int u = (useg[j] & ~15) + 8 * h2 + (lane & 7);
+      wl[j][h2] = u < N4 ? (uint32_t)u * (uint32_t)K4 * 16u : OOB;
+    }
     // This segment's 4 columns: scales (one group) and biases, fetched early.
     sone[j] = (!GROUPED && uok[j]) ? *(const floatx4 *)(sc[j] + (int64_t)e * p.N + 4 * useg[j])
                                    : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -217,23 +234,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                             : floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Stream step g = seg·steps + s: tiles 8·s + kq and 8·s + 4 + kq of the
-  // segment; the 4 lanes of a unit read 64 contiguous bytes per load.
+  // Stream step g = seg·steps + s: per instruction, 8 lanes read one unit's
+  // 8 tiles of the step (128 contiguous bytes).
+  const int lt = lane >> 3;
+  const bool odd = (lane & 8) != 0;
+  // Steps past the stream load zeros (out-of-range offsets), so every
+  // phase of the pipeline issues its loads unconditionally.
   auto issue = [&](int g, WStep &d) {
     const int seg = NS == 1 ? 0 : (g >= steps ? 1 : 0);
     const int s = g - seg * steps;
-    const int ka = s * 8 + kq, kb = ka + 4;
-    d.t0 = (uok[seg] && ka < K4) ? load_stream(wt[seg] + ka) : uint4{0, 0, 0, 0};
-    d.t1 = (uok[seg] && kb < K4) ? load_stream(wt[seg] + kb) : uint4{0, 0, 0, 0};
+    const bool live = g < gsteps;
+    const int ka = s * 8 + lt, kb = s * 8 + (lt ^ 1);
+    const uint32_t o0 = (live && ka < K4) ? wl[seg][0] + (uint32_t)ka * 16u : OOB;
+    const uint32_t o1 = (live && kb < K4) ? wl[seg][1] + (uint32_t)kb * 16u : OOB;
+    d.t0 = load_stream(wr[seg], o0);
+    d.t1 = load_stream(wr[seg], o1);
   };
-
   for (int c0 = 0; c0 < cnt; c0 += RC) {
     const int rows = min(RC, cnt - c0);
     WStep b0, b1, b2, b3;
     // The weight stream does not depend on the rows: start it first.
     issue(0, b0);
-    if (1 < gsteps) issue(1, b1);
-    if (2 < gsteps) issue(2, b2);
+    issue(1, b1);
+    issue(2, b2);
 
     // Stage this chunk's A rows (gathered through perm) in LDS.
     for (int r = wave; r < RC; r += NW) {
@@ -252,6 +275,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         *(half4 *)(ahi + r * kp + k) = h;
         if (SPLIT) *(half4 *)(alo + r * kp + k) = l;
       }
+    }
+    // Output rows of this lane's sums (rows 4·kq + q of the chunk), fetched
+    // before the stream so that no load waits inside it.
+    int orow_i[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int mm = kq * 4 + q;
+      orow_i[q] = mm < rows ? perm[p0 + c0 + mm] : 0;
     }
     __syncthreads();
 
@@ -285,7 +316,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         for (int q = 0; q < 4; q++) {
           const int mm = kq * 4 + q;
           if (mm >= rows) continue;
-          float *orow = out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * useg[seg];
+          float *orow = out + (int64_t)orow_i[q] * p.N + 4 * useg[seg];
           floatx4 v;
           if (MODE == MODE_UP) {
 #pragma unroll
@@ -311,11 +342,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         if (SPLIT) a_lo = half8{};
       }
       floatx4 *acc = GROUPED ? tmp : tot;
-      const uint32_t w0[4] = {d.t0.x, d.t0.y, d.t0.z, d.t0.w};
-      const uint32_t w1[4] = {d.t1.x, d.t1.y, d.t1.z, d.t1.w};
+      // Own tile 2kq (t0 on even lanes, t1 on odd), tile 2kq + 1 from lane ^ 8.
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const half8 bv = cvt_i8x8(w0[i], w1[i]);
+        const uint32_t own = odd ? d.t1[i] : d.t0[i];
+        const uint32_t other = swap8(odd ? d.t0[i] : d.t1[i]);
+        const half8 bv = cvt_i8x8(own, other);
         acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bv, acc[i], 0, 0, 0);
         if (SPLIT) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, bv, acc[i], 0, 0, 0);
       }
@@ -337,23 +369,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
       if (s == steps - 1) finish(seg);
     };
 
-    // Buffers rotate b0 → b1 → b2 → b3 (loads three steps ahead); every
-    // phase is guarded, no early exits.
+    // Buffers rotate b0 → b1 → b2 → b3 (loads three steps ahead). The loads
+    // are unconditional (past the stream they read zeros); only the
+    // computes are guarded.
     for (int g = 0; g < gsteps; g += 4) {
-      if (g + 3 < gsteps) issue(g + 3, b3);
+      issue(g + 3, b3);
       compute(g, b0);
-      if (g + 1 < gsteps) {
-        if (g + 4 < gsteps) issue(g + 4, b0);
-        compute(g + 1, b1);
-      }
-      if (g + 2 < gsteps) {
-        if (g + 5 < gsteps) issue(g + 5, b1);
-        compute(g + 2, b2);
-      }
-      if (g + 3 < gsteps) {
-        if (g + 6 < gsteps) issue(g + 6, b2);
-        compute(g + 3, b3);
-      }
+      issue(g + 4, b0);
+      if (g + 1 < gsteps) compute(g + 1, b1);
+      issue(g + 5, b1);
+      if (g + 2 < gsteps) compute(g + 2, b2);
+      issue(g + 6, b2);
+      if (g + 3 < gsteps) compute(g + 3, b3);
     }
     if (PAIRED) {
       // lin wavefront parks its sums; glu wavefront applies the SwiGLU.
@@ -367,7 +394,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         for (int q = 0; q < 4; q++) {
           const int mm = kq * 4 + q;
           if (mm >= rows) continue;
-          float *orow = out + (int64_t)perm[p0 + c0 + mm] * p.N + 4 * useg[0];
+          float *orow = out + (int64_t)orow_i[q] * p.N + 4 * useg[0];
           floatx4 v;
 #pragma unroll
           for (int i = 0; i < 4; i++) v[i] = swiglu(tot[i][q], park[i * WAVE + lane][q]);
