@@ -16,6 +16,11 @@
  *                                                  kernel src/core/kernels/matmul/moeQuantW.ts:188-237
  *   moe_layer        the quantized branch of EagerMoeMlp.forward after rmsNorm:
  *                    topk(router) → moeUp → moeDown  src/zoo/privacy-filter/moeMlp.ts:82-121
+ *   moe_rmsnorm      rmsNorm(x, weight, eps, {group, residual, scale})
+ *                                                  src/core/graph/ops/reduce.ts:61-92,
+ *                                                  kernel src/core/kernels/reduce/rmsNorm.ts
+ *   moe_block        the quantized EagerMoeMlp.forward whole: rmsNorm(x) →
+ *                    topk(router) → moeUp → moeDown(+x)  src/zoo/privacy-filter/moeMlp.ts:79-121
  *   moe_weights_upload / _view / _dispose / _release
  *                    a QuantExpertWeight's buffers uploaded and owned by the
  *                    library (Parameter, src/core/nn/module.ts:20-65)
@@ -87,11 +92,18 @@ MOE_API int moe_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 MOE_API const char *moe_last_error(void);
 
+/* The device's null (legacy default) stream, as a `stream` argument: the
+ * stream a caller with no stream of its own enqueues on (HIP's stream 0,
+ * torch's default stream). Work on it is ordered with the caller's; NULL
+ * instead selects the context's own non-blocking stream, which is not. */
+#define MOE_NULL_STREAM ((void *)1)
 /* A context owns one HIP stream (or borrows `stream`, a hipStream_t, when it
- * is not NULL) and the device workspace the layer needs between kernels.
+ * is not NULL; MOE_NULL_STREAM for the null stream) and the device workspace
+ * the layer needs between kernels.
  * Replaces initRunntime(root)/gpuExecutor(root) (src/core/gpu/eval.ts:80-100). */
 MOE_API int moe_ctx_create(int device, void *stream, moe_ctx **out);
-/* Switch the stream later calls enqueue on (NULL: the context's own). */
+/* Switch the stream later calls enqueue on (NULL: the context's own;
+ * MOE_NULL_STREAM: the null stream). */
 MOE_API int moe_ctx_set_stream(moe_ctx *ctx, void *stream);
 /* Grow the workspace now for layers up to these sizes, so later calls with
  * no larger shapes allocate nothing. */
@@ -141,6 +153,30 @@ MOE_API int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
               int k, int bits, int group_size_up, int group_size_down, float *route_out,
               float *out);
 
+/* EagerMoeMlp.forward for the quantized formats
+ * (src/zoo/privacy-filter/moeMlp.ts:79-121): xn = rmsNorm(x, norm_w, eps),
+ * route = topk(xn·W + b, k), out = x + moeDown(moeUp(xn, route, glu, lin),
+ * route, down). The residual is x itself, in its own dtype. x and norm_w
+ * share x_dtype (f32 or f16); norm_w is [d]; the privacy filter's eps is
+ * 1e-5 (moeMlp.ts:23). The norm's sum of squares follows this library's
+ * canonical order (see moe_rmsnorm), so the expert ids are reproducible. */
+MOE_API int moe_block(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const void *norm_w,
+                      float eps, const float *w_router, const float *b_router,
+                      const moe_expert_weight *glu, const moe_expert_weight *lin,
+                      const moe_expert_weight *down, int T, int d, int I, int E, int k, int bits,
+                      int group_size_up, int group_size_down, float *route_out, float *out);
+/* rmsNorm(x, weight, eps, {group, residual, scale})
+ * (src/core/graph/ops/reduce.ts:61-92): over each run of `group` columns of
+ * a [rows, cols] row, out = (residual + x · 1/sqrt(mean(x²) + eps) · w) · scale.
+ * x, weight, residual (NULL: none) and out share `dtype`; weight_len is
+ * `group` (one weight shared by every run) or `cols` (a slice per run).
+ * Sums in f32 in a canonical order: lane l of a 64-wide wavefront adds the
+ * squares of the quads q ≡ l (mod 64) in ascending order, the 64 lane sums
+ * meet in an xor butterfly (strides 32..1), then 1/sqrt(sum/group + eps),
+ * each operation correctly rounded. */
+MOE_API int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
+                        const void *weight, int weight_len, float eps, int group,
+                        const void *residual, float scale, void *out);
 /* Strides between the calls of moe_layer_batched, in elements of each
  * tensor (u32 words for quantW weights). 0 shares a tensor between calls. */
 typedef struct moe_call_strides {
@@ -172,7 +208,7 @@ MOE_API int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides *s
  * GpuPerfSink with perOp (src/core/gpu/perf.ts:1-23, timing.ts:62-111).
  * While enabled, every launch group is bracketed by a HIP event pair.
  * moe_prof_read waits for the stream and returns, per group (index: 0 topk,
- * 1 router, 2 dispatch, 3 up, 4 down, 5 combine; 8 slots), the summed
+ * 1 router, 2 dispatch, 3 up, 4 down, 5 combine, 6 norm; 8 slots), the summed
  * milliseconds and the number of timed groups; reset != 0 clears them. */
 MOE_API int moe_prof_enable(moe_ctx *ctx, int on);
 MOE_API int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *count_out);

@@ -29,6 +29,13 @@
  *   orc_*_f32ref           agreement with the f64 forms at the reference
  *                          test's tolerance (atol 1e-5·K, rtol 1e-4)
  *   orc_dispatch           brute-force stable argsort
+ *   orc_rmsnorm            the reference test's f64 formula at its tolerance
+ *                          (test/core/kernels/reduce/rmsNorm.gpu.test.ts:33-61,
+ *                          atol 1e-6, rtol 1e-5) on its shapes and options;
+ *                          closed forms (constant rows, eps dominance, scale
+ *                          and residual); the lane-order sum against a
+ *                          different association, which it must not equal in
+ *                          general
  */
 #include <math.h>
 #include <stdint.h>
@@ -432,4 +439,53 @@ EXPORT void orc_moe_layer_f64(const float *x, const float *router_w, const float
   free(logits);
   orc_moe_up_f64(x, route, glu_w, glu_s, glu_b, lin_w, lin_s, lin_b, T, d, I, E, k, bits, g_up, act);
   orc_moe_down_f64(act, route, down_w, down_s, down_b, residual, T, I, d, E, k, bits, g_down, out);
+}
+
+/* ------------------------------------------------------------------ norm */
+
+/* src/core/graph/ops/reduce.ts:61-92 and src/core/kernels/reduce/rmsNorm.ts
+ * :84-140 — rmsNorm(x, weight, eps, {group, residual, scale}): over each
+ * run of `group` columns, inv = 1/sqrt(Σx²/group + eps), then
+ * v = x·inv·w (left to right), v = v + residual, out = v·scale.
+ * The sum follows this library's canonical f32 order (the reference sums in
+ * a device-dependent subgroup or tree order): 64 lane sums, lane l adding
+ * x·x for the quads q ≡ l (mod 64) of the run in ascending order (within a
+ * quad ascending), no fused multiply-add; then an xor butterfly over the
+ * lane sums, strides 32, 16, …, 1, read at lane 0; every operation one IEEE
+ * f32 rounding. w is `group` long (shared by every run) or `cols` long (a
+ * slice per run). Inputs and outputs are f32; an f16 caller rounds them. */
+EXPORT void orc_rmsnorm(const float *x, int64_t rows, int cols, int group, const float *w,
+                        int wlen, float eps, const float *res, float scale, float *out) {
+  float lanes[64];
+  for (int64_t r = 0; r < rows; r++)
+    for (int g0 = 0; g0 < cols; g0 += group) {
+      const float *xr = x + r * cols + g0;
+      for (int l = 0; l < 64; l++) {
+        float s = 0.0f;
+        for (int q = l; 4 * q < group; q += 64)
+          for (int j = 0; j < 4; j++) {
+            int i = 4 * q + j;
+            if (i < group) {
+              float sq = xr[i] * xr[i];
+              s = s + sq;
+            }
+          }
+        lanes[l] = s;
+      }
+      for (int m = 32; m >= 1; m >>= 1) {
+        float nxt[64];
+        for (int l = 0; l < 64; l++) nxt[l] = lanes[l] + lanes[l ^ m];
+        memcpy(lanes, nxt, sizeof(lanes));
+      }
+      float mean = lanes[0] / (float)group;
+      float inv = 1.0f / sqrtf(mean + eps);
+      const float *wr = wlen == group ? w : w + g0;
+      for (int i = 0; i < group; i++) {
+        float v = xr[i] * inv;
+        v = v * wr[i];
+        if (res) v = v + res[r * cols + g0 + i];
+        v = v * scale;
+        out[r * cols + g0 + i] = v;
+      }
+    }
 }

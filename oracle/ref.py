@@ -56,6 +56,7 @@ def lib():
         "orc_moe_layer_f64": [_f32p, _f32p, F, _u32p, _f32p, F, _u32p, _f32p, F, _u32p, _f32p, F,
                               F, I, I, I, I, I, I, I, I, _f32p, _f32p, _f32p],
     }
+    sigs["orc_rmsnorm"] = [_f32p, I64, I, I, _f32p, I, ctypes.c_float, F, ctypes.c_float, _f32p]
     for name, args in sigs.items():
         fn = getattr(L, name)
         fn.argtypes = args
@@ -147,3 +148,15 @@ def dispatch(route, E):
     offsets = np.zeros(E + 1, np.int32)
     lib().orc_dispatch(_f(route), T, k, E, perm, inv, offsets)
     return perm, inv, offsets
+
+
+def rmsnorm(x, weight, eps, group=None, residual=None, scale=1.0, dtype=np.float32):
+    """rmsNorm in the canonical order. x, weight, residual hold values of
+    `dtype` (f32 or f16); the result is rounded to `dtype` as the kernel
+    stores it."""
+    rows, cols = x.shape
+    group = cols if group is None else group
+    out = np.zeros((rows, cols), np.float32)
+    lib().orc_rmsnorm(_f(x), rows, cols, group, _f(weight), int(np.asarray(weight).size),
+                      float(eps), _f(residual), float(scale), out)
+    return out.astype(dtype)

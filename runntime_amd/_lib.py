@@ -13,6 +13,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmoe.so")
 
 MOE_F32 = 0
 MOE_F16 = 1
+# MOE_NULL_STREAM: the null (legacy default) stream as a stream argument.
+MOE_NULL_STREAM = 1
 
 # Every symbol include/runntime_moe.h declares.
 EXPORTED = (
@@ -21,8 +23,9 @@ EXPORTED = (
     "moe_up", "moe_down", "moe_layer", "moe_dispatch", "moe_prof_enable", "moe_prof_read",
     "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
     "moe_weights_upload", "moe_weights_view", "moe_weights_dispose", "moe_weights_release",
+    "moe_block", "moe_rmsnorm",
 )
-PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine")
+PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine", "norm")
 
 
 class CallStridesC(ctypes.Structure):
@@ -79,6 +82,9 @@ def load() -> ctypes.CDLL:
             "moe_weights_view": ([P, W], I),
             "moe_weights_dispose": ([P], I),
             "moe_weights_release": ([P], I),
+            "moe_block": ([P, P, I, P, ctypes.c_float, P, P, W, W, W, I, I, I, I, I, I, I, I, P,
+                           P], I),
+            "moe_rmsnorm": ([P, P, I, I, I, P, I, ctypes.c_float, I, P, ctypes.c_float, P], I),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)
@@ -98,7 +104,10 @@ def check(rc: int) -> None:
 
 def context(device: int, stream_handle: int) -> int:
     """The library context of `device`, switched to enqueue on `stream_handle`
-    (a hipStream_t as an int, 0 for the context's own stream)."""
+    (a hipStream_t as an int). 0 is the null stream, as torch reports its
+    default stream: the library then enqueues on that same null stream, so
+    its kernels are ordered with torch's work (the context's own stream is
+    non-blocking and would not be)."""
     lib = load()
     with _lock:
         ctx = _ctxs.get(device)
@@ -107,5 +116,5 @@ def context(device: int, stream_handle: int) -> int:
             check(lib.moe_ctx_create(device, None, ctypes.byref(out)))
             ctx = out.value
             _ctxs[device] = ctx
-    check(lib.moe_ctx_set_stream(ctx, stream_handle or None))
+    check(lib.moe_ctx_set_stream(ctx, stream_handle or MOE_NULL_STREAM))
     return ctx

@@ -25,8 +25,9 @@ COMMON = [
 # order with explicit fmaf(): nothing else may be fused there.
 PER_FILE = {
     "router.hip": ["-ffp-contract=off"],
+    "norm.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "pack.hip"]
+SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "pack.hip", "norm.hip"]
 
 
 def _compile(src: str) -> str:

@@ -5,8 +5,10 @@ graph ops (packages/runntime/src/core/graph/ops/):
   topk(x, k)                                  reduce.ts:93-100
   moeUp(x, route, glu, lin, {bits, groupSize})  matmul.ts:220-244
   moeDown(act, route, out, residual, opts)    matmul.ts:246-272
+  rmsNorm(x, weight, eps, {group, residual, scale})  reduce.ts:61-92
 plus the fused layer (EagerMoeMlp's quantized branch, zoo/privacy-filter/
-moeMlp.ts:82-121) and the router+topk fusion.
+moeMlp.ts:82-121), the whole block with its pre-norm (moe_block,
+moeMlp.ts:79-121) and the router+topk fusion.
 
 The reference builds lazy nodes and runs them later; here each op enqueues
 its HIP kernels at once on torch's current stream and returns the output
@@ -258,6 +260,76 @@ def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWei
                              _ptr(router_b), ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn),
                              _ptr(residual), t, d, i, e, k, bits, gu, gd, route.data_ptr(),
                              out.data_ptr()))
+    return (out, route) if return_route else out
+
+
+def rmsNorm(x, weight, eps: float = 1e-6, opts=None) -> torch.Tensor:
+    """RMSNorm over the last dim: x · rsqrt(mean(x²) + eps) · weight, summed
+    in f32 even for f16 x (src/core/graph/ops/reduce.ts:61-92). opts.group
+    normalizes each run of `group` columns on its own; the weight is then
+    `group` long (shared by every run) or N long (a slice per run).
+    opts.residual and opts.scale turn the output into
+    (residual + norm(x)) · scale. Same dtype as x."""
+    opts = opts or {}
+    m, n, dtype = _want2d("rmsNorm", x, ("f32", "f16"))
+    group = opts.get("group", n)
+    residual = opts.get("residual")
+    scale = opts.get("scale", 1)
+    if not isinstance(group, int) or group < 1 or n % group != 0:
+        raise ValueError(f"rmsNorm: group {group} must divide the row width {n}")
+    wl = weight.numel()
+    if _dtype_name(weight) != dtype or (wl != group and wl != n):
+        lens = f"{n}" if group == n else f"{group} or {n}"
+        raise ValueError(
+            f"rmsNorm: weight must be {dtype} with {lens} elems, got ({wl},{_dtype_name(weight)})")
+    if not (eps > 0):
+        raise ValueError(f"rmsNorm: eps must be positive, got {eps}")
+    if residual is not None and (_dtype_name(residual) != dtype or residual.numel() != m * n):
+        raise ValueError(f"rmsNorm: residual must be {dtype} [{m}, {n}]")
+    dev = _device_of(x, weight, residual)
+    out = torch.empty((m, n), dtype=x.dtype, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_rmsnorm(_ctx(dev), x.data_ptr(), _xdtype(x), m, n, weight.data_ptr(), wl,
+                               float(eps), group, _ptr(residual), float(scale), out.data_ptr()))
+    return out
+
+
+def moe_block(x, norm_w, eps, router_w, router_b, glu: QuantExpertWeight,
+              lin: QuantExpertWeight, down: QuantExpertWeight, k: int, bits: int = 8,
+              group_size_up=None, group_size_down=None, return_route: bool = False):
+    """EagerMoeMlp.forward for the quantized formats
+    (src/zoo/privacy-filter/moeMlp.ts:79-121) in one call:
+    xn = rmsNorm(x, norm_w, eps); route = topk(xn·Wr + br, k);
+    out = moeDown(moeUp(xn, route, glu, lin), route, down, x). The residual
+    is x in its own dtype; out is f32 [T, d]. The privacy filter's eps is
+    1e-5 (moeMlp.ts:23)."""
+    t, d, dtype = _want2d("moe_block", x, ("f32", "f16"))
+    if _dtype_name(norm_w) != dtype or norm_w.numel() != d:
+        raise ValueError(f"rmsNorm: weight must be {dtype} with {d} elems, got "
+                         f"({norm_w.numel()},{_dtype_name(norm_w)})")
+    if not (eps > 0):
+        raise ValueError(f"rmsNorm: eps must be positive, got {eps}")
+    rw = _dims(router_w)
+    if _dtype_name(router_w) != "f32" or len(rw) != 2 or rw[0] != d:
+        raise ValueError(f"moe_block: router weight must be f32 [{d}, E]")
+    e = rw[1]
+    if not isinstance(glu.w, QuantW) or glu.w.dims[0] != e * d:
+        raise ValueError(f"moe_block: glu.w must be a quantW [E·{d}, I] weight")
+    i = glu.w.dims[1]
+    gu = group_size_up or d
+    gd = group_size_down or i
+    route = torch.empty((t, 2 * k), dtype=torch.float32, device=x.device)
+    _check_expert_weight("moe_block", glu, d, route, t, k, {"bits": bits, "groupSize": gu})
+    _check_expert_weight("moe_block", lin, d, route, t, k, {"bits": bits, "groupSize": gu})
+    _check_expert_weight("moe_block", down, i, route, t, k, {"bits": bits, "groupSize": gd})
+    dev = _device_of(x, norm_w, router_w, router_b, glu.w, lin.w, down.w)
+    out = torch.empty((t, d), dtype=torch.float32, device=dev)
+    g, l_, dn = _weight_c(glu), _weight_c(lin), _weight_c(down)
+    lib = _lib.load()
+    _lib.check(lib.moe_block(_ctx(dev), x.data_ptr(), _xdtype(x), norm_w.data_ptr(), float(eps),
+                             router_w.data_ptr(), _ptr(router_b), ctypes.byref(g),
+                             ctypes.byref(l_), ctypes.byref(dn), t, d, i, e, k, bits, gu, gd,
+                             route.data_ptr(), out.data_ptr()))
     return (out, route) if return_route else out
 
 

@@ -481,10 +481,11 @@ __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
 
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s], slots in order; rows of
 // ids that are not experts contribute nothing. Reads, never scatters.
+template <typename RT>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, int64_t y_cs,
                                                  int parts, int64_t part_cs,
                                                  const float *__restrict__ route, int64_t route_cs,
-                                                 const float *__restrict__ residual, int64_t res_cs,
+                                                 const RT *__restrict__ residual, int64_t res_cs,
                                                  int T, int N, int E, int k,
                                                  float *__restrict__ out, int64_t out_cs) {
   const int call = blockIdx.z;
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
   if (n >= N) return;
   y += call * y_cs;
   route += call * route_cs;
-  float acc = residual ? residual[call * res_cs + (int64_t)t * N + n] : 0.f;
+  float acc = residual ? (float)residual[call * res_cs + (int64_t)t * N + n] : 0.f;
   for (int s = 0; s < k; s++) {
     const int64_t asg = (int64_t)t * k + s;
     if (route_expert(route, asg, k, E) < 0) continue;
@@ -509,11 +510,19 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
 // template parameter so every slot's loads are in flight together (a
 // runtime count leaves the slot array in scratch memory, one load at a
 // time); the same order of operations per column.
-template <int KK>
+// Four residual values as f32.
+__device__ __forceinline__ float4 load4(const float *p) { return *(const float4 *)p; }
+__device__ __forceinline__ float4 load4(const _Float16 *p) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 v = *(const h4 *)p;
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+template <int KK, typename RT>
 __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, int64_t y_cs,
                                                   int parts, int64_t part_cs,
                                                   const float *__restrict__ route, int64_t route_cs,
-                                                  const float *__restrict__ residual, int64_t res_cs,
+                                                  const RT *__restrict__ residual, int64_t res_cs,
                                                   int T, int N, int E,
                                                   float *__restrict__ out, int64_t out_cs) {
   const int call = blockIdx.z;
@@ -533,7 +542,7 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, i
     v[s] = *(const float4 *)&y[asg * N + n];
   }
   // The residual after the slot loads, so they all wait together.
-  float4 acc = residual ? *(const float4 *)&residual[call * res_cs + (int64_t)t * N + n]
+  float4 acc = residual ? load4(&residual[call * res_cs + (int64_t)t * N + n])
                         : make_float4(0.f, 0.f, 0.f, 0.f);
   for (int q = 1; q < parts; q++) {
 #pragma unroll
@@ -678,21 +687,19 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   return launch_mode<MODE_DOWN>(ea, p, s);
 }
 
-int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, const float *route,
-                   int64_t route_cs,
-                   const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
-                   int64_t out_cs, int calls, hipStream_t s) {
-  MOE_NONNULL(y);
-  MOE_NONNULL(route);
-  MOE_NONNULL(out);
+template <typename RT>
+static int combine_typed(const float *y, int64_t y_cs, int parts, int64_t part_cs,
+                         const float *route, int64_t route_cs, const RT *residual, int64_t res_cs,
+                         int T, int N, int E, int k, float *out, int64_t out_cs, int calls,
+                         hipStream_t s) {
   auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  const int pp = parts < 1 ? 1 : parts;
   if (N % 4 == 0 && (k <= 8 || k == 16) && a16(y) && a16(out) && (!residual || a16(residual)) &&
       y_cs % 4 == 0 && part_cs % 4 == 0 && out_cs % 4 == 0 && res_cs % 4 == 0) {
     dim3 grid(T, (N / 4 + 255) / 256, calls), block(256);
-    const int pp = parts < 1 ? 1 : parts;
 #define COMBINE4(KK_)                                                                        \
   case KK_:                                                                                  \
-    hipLaunchKernelGGL(k_combine4<KK_>, grid, block, 0, s, y, y_cs, pp, part_cs, route,      \
+    hipLaunchKernelGGL((k_combine4<KK_, RT>), grid, block, 0, s, y, y_cs, pp, part_cs, route, \
                        route_cs, residual, res_cs, T, N, E, out, out_cs);                    \
     return 0;
     switch (k) {
@@ -702,9 +709,23 @@ int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, con
 #undef COMBINE4
   }
   dim3 grid(T, (N + 255) / 256, calls), block(256);
-  hipLaunchKernelGGL(k_combine, grid, block, 0, s, y, y_cs, parts < 1 ? 1 : parts, part_cs, route,
-                     route_cs, residual, res_cs, T, N, E, k, out, out_cs);
+  hipLaunchKernelGGL(k_combine<RT>, grid, block, 0, s, y, y_cs, pp, part_cs, route, route_cs,
+                     residual, res_cs, T, N, E, k, out, out_cs);
   return 0;
+}
+
+int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, const float *route,
+                   int64_t route_cs, const void *residual, moe_dtype res_dtype, int64_t res_cs,
+                   int T, int N, int E, int k, float *out, int64_t out_cs, int calls,
+                   hipStream_t s) {
+  MOE_NONNULL(y);
+  MOE_NONNULL(route);
+  MOE_NONNULL(out);
+  if (res_dtype == MOE_F16)
+    return combine_typed(y, y_cs, parts, part_cs, route, route_cs, (const _Float16 *)residual,
+                         res_cs, T, N, E, k, out, out_cs, calls, s);
+  return combine_typed(y, y_cs, parts, part_cs, route, route_cs, (const float *)residual, res_cs,
+                       T, N, E, k, out, out_cs, calls, s);
 }
 
 int launch_zero(float *p, size_t n, hipStream_t s) {

@@ -24,7 +24,7 @@ extern "C" int moe_version(void) { return MOE_VERSION; }
 // ------------------------------------------------------------------ timing
 
 const char *const PROF_NAMES[PROF_GROUPS] = {"topk", "router", "dispatch", "up",
-                                             "down", "combine", "", ""};
+                                             "down", "combine", "norm", ""};
 
 static hipEvent_t prof_event(moe_ctx *c) {
   if (!c->prof_free.empty()) {
@@ -94,7 +94,9 @@ extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
   MOE_HIP_CHECK(hipSetDevice(device));
   moe_ctx *c = new moe_ctx();
   c->device = device;
-  if (stream) {
+  if (stream == MOE_NULL_STREAM) {
+    c->stream = nullptr;  // HIP's null stream
+  } else if (stream) {
     c->stream = (hipStream_t)stream;
   } else {
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
@@ -121,11 +123,17 @@ static int check_ctx(moe_ctx *ctx, const char *op) {
 extern "C" int moe_ctx_set_stream(moe_ctx *ctx, void *stream) {
   int rc = check_ctx(ctx, "moe_ctx_set_stream");
   if (rc) return rc;
-  ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
-  if (!ctx->stream) {
-    MOE_HIP_CHECK(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking));
-    ctx->stream = ctx->own_stream;
+  if (stream == MOE_NULL_STREAM) {
+    ctx->stream = nullptr;  // HIP's null stream
+    return MOE_OK;
   }
+  if (stream) {
+    ctx->stream = (hipStream_t)stream;
+    return MOE_OK;
+  }
+  if (!ctx->own_stream)
+    MOE_HIP_CHECK(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking));
+  ctx->stream = ctx->own_stream;
   return MOE_OK;
 }
 
@@ -145,7 +153,7 @@ int moe_ws_ensure(moe_ctx *ctx, size_t bytes) {
 extern "C" int moe_ctx_destroy(moe_ctx *ctx) {
   if (!ctx) return MOE_OK;
   (void)hipSetDevice(ctx->device);
-  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
   for (auto &r : ctx->prof_pending) {
     (void)hipEventDestroy(r.begin);
@@ -208,12 +216,14 @@ struct LayerWs {
   float *partial = nullptr;
   float *act = nullptr;
   float *y = nullptr;
+  void *xn = nullptr;  // normalised input of moe_block
 };
 
 // Workspace for `calls` calls over T tokens each (A = T·k assignments per
 // call). Sections that a call does not need have size 0.
 static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_floats,
-                   size_t partial_floats, size_t act_floats, size_t y_floats, LayerWs &L) {
+                   size_t partial_floats, size_t act_floats, size_t y_floats, LayerWs &L,
+                   size_t xn_bytes = 0) {
   const int A = T * k;
   const int nblk = (A + DISPATCH_TILE - 1) / DISPATCH_TILE;
   const size_t C = (size_t)calls;
@@ -229,6 +239,7 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   size_t o_part = p.take(sizeof(float) * C * partial_floats);
   size_t o_actv = p.take(sizeof(float) * C * act_floats);
   size_t o_y = p.take(sizeof(float) * C * y_floats);
+  size_t o_xn = p.take(C * xn_bytes);
   int rc = moe_ws_ensure(ctx, p.off);
   if (rc) return rc;
   char *b = ctx->ws;
@@ -246,6 +257,7 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   L.partial = partial_floats ? (float *)(b + o_part) : nullptr;
   L.act = act_floats ? (float *)(b + o_actv) : nullptr;
   L.y = y_floats ? (float *)(b + o_y) : nullptr;
+  L.xn = xn_bytes ? (void *)(b + o_xn) : nullptr;
   return MOE_OK;
 }
 
@@ -413,8 +425,8 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
   }
   {
     ProfScope ps(ctx, PG_COMBINE);
-    if ((rc = launch_combine(L.y, 0, ea.parts, (int64_t)T * k * N, route, 0, residual, 0, T, N, E,
-                             k, out, 0, 1, ctx->stream)))
+    if ((rc = launch_combine(L.y, 0, ea.parts, (int64_t)T * k * N, route, 0, residual, MOE_F32, 0,
+                             T, N, E, k, out, 0, 1, ctx->stream)))
       return rc;
   }
   return after_launch("moeDown");
@@ -422,23 +434,34 @@ extern "C" int moe_down(moe_ctx *ctx, const float *act, const float *route,
 
 static const moe_call_strides kZeroStrides = {};
 
-extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides *st,
-                                 const void *x, moe_dtype x_dtype, const float *w_router,
-                                 const float *b_router, const moe_expert_weight *glu,
-                                 const moe_expert_weight *lin, const moe_expert_weight *down,
-                                 const float *residual, int T, int d, int I, int E, int k,
-                                 int bits, int group_size_up, int group_size_down,
-                                 float *route_out, float *out) {
-  int rc = check_ctx(ctx, "moe_layer");
+// The block's pre-norm: xn = rmsNorm(x, weight, eps) over whole rows.
+struct PreNorm {
+  const void *weight;  // [d], x's dtype
+  float eps;
+};
+
+// The routed layer (moe_layer_batched), optionally behind the block's
+// pre-norm (moe_block: one call). The residual is f32 or f16.
+static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_strides *st,
+                      const void *x, moe_dtype x_dtype, const PreNorm *norm,
+                      const float *w_router, const float *b_router, const moe_expert_weight *glu,
+                      const moe_expert_weight *lin, const moe_expert_weight *down,
+                      const void *residual, moe_dtype res_dtype, int T, int d, int I, int E,
+                      int k, int bits, int group_size_up, int group_size_down, float *route_out,
+                      float *out) {
+  const std::string o(op);
+  int rc = check_ctx(ctx, op);
   if (rc) return rc;
-  if ((rc = check_k("moe_layer", k, E, true))) return rc;
-  if ((rc = check_weight("moe_layer", glu, d, I, E, bits, group_size_up))) return rc;
-  if ((rc = check_weight("moe_layer", lin, d, I, E, bits, group_size_up))) return rc;
-  if ((rc = check_weight("moe_layer", down, I, d, E, bits, group_size_down))) return rc;
-  REQUIRE(T >= 1, "moe_layer: T must be at least 1");
-  REQUIRE(calls >= 1 && calls <= 65535, "moe_layer: calls must be in 1..65535, got " + S(calls));
-  REQUIRE(E <= ROUTER_MAX_E, "moe_layer: more than " + S(ROUTER_MAX_E) + " experts");
-  REQUIRE(x && w_router && out, "moe_layer: NULL tensor");
+  if ((rc = check_k(op, k, E, true))) return rc;
+  if ((rc = check_weight(op, glu, d, I, E, bits, group_size_up))) return rc;
+  if ((rc = check_weight(op, lin, d, I, E, bits, group_size_up))) return rc;
+  if ((rc = check_weight(op, down, I, d, E, bits, group_size_down))) return rc;
+  REQUIRE(T >= 1, o + ": T must be at least 1");
+  REQUIRE(calls >= 1 && calls <= 65535, o + ": calls must be in 1..65535, got " + S(calls));
+  REQUIRE(E <= ROUTER_MAX_E, o + ": more than " + S(ROUTER_MAX_E) + " experts");
+  REQUIRE(x && w_router && out, o + ": NULL tensor");
+  REQUIRE(x_dtype == MOE_F32 || x_dtype == MOE_F16, o + ": x must be f32 or f16");
+  REQUIRE(!norm || calls == 1, o + ": the pre-norm runs one call at a time");
   if (!st) st = &kZeroStrides;
   if (calls > 1)
     REQUIRE(st->x != 0 && st->out != 0 && (!route_out || st->route != 0),
@@ -498,9 +521,20 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   dn.out_cs = (int64_t)dn.parts * A * d;
 
   LayerWs L;
+  const size_t esize = x_dtype == MOE_F16 ? 2 : 4;
   if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
-                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L)))
+                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L,
+                    norm ? (size_t)T * d * esize : 0)))
     return rc;
+  hipStream_t s = ctx->stream;
+  if (norm) {
+    // The router and the gate/up product read xn; the residual stays x.
+    ProfScope ps(ctx, PG_NORM);
+    NormArgs na{x, norm->weight, nullptr, L.xn, x_dtype, T, d, d, d, norm->eps, 1.0f};
+    if ((rc = launch_rmsnorm(na, s))) return rc;
+    x = L.xn;
+    up.a = L.xn;
+  }
   float *route = route_out ? route_out : L.route;
   const int64_t route_cs = route_out ? st->route : (int64_t)T * 2 * k;
   up.route = dn.route = route;
@@ -508,7 +542,6 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   up.out = L.act;
   dn.a = L.act;
   dn.out = L.y;
-  hipStream_t s = ctx->stream;
   bool dispatched = false;
   {
     ProfScope ps(ctx, PG_ROUTER);
@@ -531,10 +564,59 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   {
     ProfScope ps(ctx, PG_COMBINE);
     if ((rc = launch_combine(L.y, dn.out_cs, dn.parts, (int64_t)A * d, route, route_cs, residual,
-                             st->residual, T, d, E, k, out, st->out, calls, s)))
+                             res_dtype, st->residual, T, d, E, k, out, st->out, calls, s)))
       return rc;
   }
-  return after_launch("moe_layer");
+  return after_launch(op);
+}
+
+extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides *st,
+                                 const void *x, moe_dtype x_dtype, const float *w_router,
+                                 const float *b_router, const moe_expert_weight *glu,
+                                 const moe_expert_weight *lin, const moe_expert_weight *down,
+                                 const float *residual, int T, int d, int I, int E, int k,
+                                 int bits, int group_size_up, int group_size_down,
+                                 float *route_out, float *out) {
+  return layer_impl("moe_layer", ctx, calls, st, x, x_dtype, nullptr, w_router, b_router, glu,
+                    lin, down, residual, MOE_F32, T, d, I, E, k, bits, group_size_up,
+                    group_size_down, route_out, out);
+}
+
+extern "C" int moe_block(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const void *norm_w,
+                         float eps, const float *w_router, const float *b_router,
+                         const moe_expert_weight *glu, const moe_expert_weight *lin,
+                         const moe_expert_weight *down, int T, int d, int I, int E, int k,
+                         int bits, int group_size_up, int group_size_down, float *route_out,
+                         float *out) {
+  REQUIRE(norm_w, "moe_block: NULL norm weight");
+  REQUIRE(eps > 0.f, "moe_block: eps must be positive, got " + std::to_string(eps));
+  const PreNorm norm{norm_w, eps};
+  return layer_impl("moe_block", ctx, 1, nullptr, x, x_dtype, &norm, w_router, b_router, glu,
+                    lin, down, x, x_dtype, T, d, I, E, k, bits, group_size_up, group_size_down,
+                    route_out, out);
+}
+
+extern "C" int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
+                           const void *weight, int weight_len, float eps, int group,
+                           const void *residual, float scale, void *out) {
+  int rc = check_ctx(ctx, "rmsNorm");
+  if (rc) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "rmsNorm: dtype must be f32 or f16");
+  REQUIRE(rows >= 1 && cols >= 1, "rmsNorm: rows and cols must be positive");
+  REQUIRE(group >= 1 && cols % group == 0,
+          "rmsNorm: group " + S(group) + " must divide the row width " + S(cols));
+  REQUIRE(weight_len == group || weight_len == cols,
+          "rmsNorm: weight must be " + std::string(dtype == MOE_F16 ? "f16" : "f32") + " with " +
+              (group == cols ? S(cols) : S(group) + " or " + S(cols)) + " elems, got (" +
+              S(weight_len) + ")");
+  REQUIRE(eps > 0.f, "rmsNorm: eps must be positive, got " + std::to_string(eps));
+  REQUIRE(x && weight && out, "rmsNorm: NULL tensor");
+  {
+    ProfScope ps(ctx, PG_NORM);
+    NormArgs na{x, weight, residual, out, dtype, rows, cols, group, weight_len, eps, scale};
+    if ((rc = launch_rmsnorm(na, ctx->stream))) return rc;
+  }
+  return after_launch("rmsNorm");
 }
 
 extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,

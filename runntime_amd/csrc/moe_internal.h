@@ -48,7 +48,9 @@ struct moe_ctx {
 };
 
 // Kernel groups the timing sink reports.
-enum ProfGroup { PG_TOPK = 0, PG_ROUTER = 1, PG_DISPATCH = 2, PG_UP = 3, PG_DOWN = 4, PG_COMBINE = 5 };
+enum ProfGroup {
+  PG_TOPK = 0, PG_ROUTER = 1, PG_DISPATCH = 2, PG_UP = 3, PG_DOWN = 4, PG_COMBINE = 5, PG_NORM = 6
+};
 extern const char *const PROF_NAMES[PROF_GROUPS];
 
 // Brackets the launches of one group with events when timing is on.
@@ -192,8 +194,23 @@ int launch_zero(float *p, size_t n, hipStream_t s);
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s] per call.
 int launch_pack_quantw(const int8_t *ints, int E, int k, int n, int bits, uint32_t *words,
                        hipStream_t s);
-// y holds `parts` partial products, part_cs floats apart (per call).
+// y holds `parts` partial products, part_cs floats apart (per call). The
+// residual is f32 or f16 (res_dtype), or NULL.
 int launch_combine(const float *y, int64_t y_cs, int parts, int64_t part_cs, const float *route,
-                   int64_t route_cs,
-                   const float *residual, int64_t res_cs, int T, int N, int E, int k, float *out,
-                   int64_t out_cs, int calls, hipStream_t s);
+                   int64_t route_cs, const void *residual, moe_dtype res_dtype, int64_t res_cs,
+                   int T, int N, int E, int k, float *out, int64_t out_cs, int calls,
+                   hipStream_t s);
+
+// RMSNorm over runs of `group` columns (norm.hip). x, weight, residual and
+// out share `dtype`; weight is `group` long (shared by every run) or `cols`
+// long (a slice per run); residual may be NULL.
+struct NormArgs {
+  const void *x;
+  const void *weight;
+  const void *residual;
+  void *out;
+  moe_dtype dtype;
+  int rows, cols, group, weight_len;
+  float eps, scale;
+};
+int launch_rmsnorm(const NormArgs &a, hipStream_t s);

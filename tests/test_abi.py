@@ -176,3 +176,27 @@ def test_weights_null_handle_paths():
     assert lib.moe_weights_view(None, ctypes.byref(v)) == 3
     assert b"handle is NULL" in lib.moe_last_error()
     assert lib.moe_weights_release(None) == 0
+
+
+@pytest.mark.parametrize("case", [
+    dict(x=_input([4])[None, None], error=r"rmsNorm: expected a 2D f32 or f16 tensor"),
+    dict(opts={"group": 3}, error=r"rmsNorm: group 3 must divide the row width 8"),
+    dict(w=_input([4]), error=r"rmsNorm: weight must be f32 with 8 elems, got \(4,f32\)"),
+    dict(w=_input([3]), opts={"group": 4}, error=r"weight must be f32 with 4 or 8 elems, got \(3,f32\)"),
+    dict(w=_input([8]).half(), error=r"weight must be f32 with 8 elems, got \(8,f16\)"),
+    dict(eps=0, error=r"rmsNorm: eps must be positive, got 0"),
+    dict(opts={"residual": _input([4, 4])}, error=r"rmsNorm: residual must be f32 \[4, 8\]"),
+])
+def test_rmsnorm_rejects(case):
+    # test/core/graph/ops/reduce.test.ts:116-170 and ops/reduce.ts:67-91
+    with pytest.raises(ValueError, match=case["error"]):
+        rt.rmsNorm(case.get("x", _input([4, 8])), case.get("w", _input([8])), case.get("eps", 1e-6),
+                   case.get("opts"))
+
+
+def test_moe_block_rejects_a_bad_norm_weight():
+    x = _input([2, 8])
+    with pytest.raises(ValueError, match=r"rmsNorm: weight must be f32 with 8 elems"):
+        rt.moe_block(x, _input([4]), 1e-5, _input([8, 2]), None, GLU, LIN, OUT, 2)
+    with pytest.raises(ValueError, match=r"rmsNorm: eps must be positive"):
+        rt.moe_block(x, _input([8]), 0.0, _input([8, 2]), None, GLU, LIN, OUT, 2)

@@ -494,3 +494,25 @@ def test_upload_rejects_an_empty_shape():
                                 0, 4, 4, 8, 4)
     assert ei.value.code == "INVALID_ARGUMENT"
     assert "no elements" in str(ei.value)
+
+
+def test_results_are_ordered_with_torchs_default_stream():
+    """Torch reports its default stream as handle 0; the library must then
+    enqueue on that same null stream. Torch work issued right after a call
+    (a comparison, a host copy) with no explicit synchronisation sees the
+    finished results. A ~2 ms prefill layer makes any missing ordering show:
+    the copy would run while the kernels still write."""
+    cfg = CONFIGS[4]
+    say("ordering with the default stream, config 4 layer")
+    inp = make_inputs(cfg, seed=41)
+    assert torch.cuda.current_stream().cuda_stream == 0
+    out = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                       inp.residual, cfg.k)
+    again = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                         inp.residual, cfg.k)
+    same = torch.equal(out, again)  # a torch kernel, queued right behind the layer
+    first = out.cpu()               # a copy on the default stream, no synchronize
+    torch.cuda.synchronize()
+    assert same
+    assert torch.equal(first, out.cpu())
+    assert first.abs().sum() > 0
