@@ -270,26 +270,33 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     value = tokens_per_step * args.steps / elapsed
 
-    # Experts touched per call: every token routes to k distinct experts.
+    # Experts touched per call: a single token routes to k distinct experts;
+    # for more tokens, the distinct ids of each input set's actual route
+    # (the same router as the layer's), averaged over the sets.
     if args.config == 2:
         active_per_call = cfg.k
         calls = tokens_per_step
         W = args.calls_per_launch
     else:
-        active_per_call = min(cfg.E, cfg.T * cfg.k)
+        counts = []
+        for w in sets:
+            r = rt.router_topk(w.x, w.router_w, w.router_b, cfg.k)
+            counts.append(int(torch.unique(r[:, :cfg.k]).numel()))
+        active_per_call = sum(counts) / len(counts)
         calls = tokens_per_step // cfg.T
     up_ms, up_n = groups.get("up", (0.0, 0))
     up_avg_s = up_ms / max(up_n, 1) / 1e3
     traffic, traffic_src = profiled_traffic(
         args.config, args.config != 2 or args.calls_per_launch == 1000)
     if args.config in (2, 3):
-        per_launch = up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1)
+        per_launch = round(up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1))
         achieved = per_launch / up_avg_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "traffic_source": traffic_src,
                     "kernel": "k_expert_skinny<up> (gate/up + SwiGLU)",
                     "algorithmic_bytes_per_launch": per_launch,
+                    "active_experts_per_call": active_per_call,
                     "avg_launch_us": round(up_avg_s * 1e6, 2)}
         layer_frac = layer_bytes(cfg, active_per_call) * calls / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS
     else:

@@ -155,14 +155,21 @@ __device__ __forceinline__ uint32_t swap8(uint32_t v) {
 // sums wait in LDS for the SwiGLU epilogue.
 // GROUPED: scales change along K (groupSize < K), so partial sums are
 // scaled per group; otherwise one scale per column is applied at the end.
-template <int MODE, typename AT, bool GROUPED, int NW, int NS>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_skinny(
+// KS = 2 splits every stream over two wavefronts, each taking half of K
+// (more wavefronts in flight when few experts and columns are active); at
+// each segment end the second half's sums meet the first's in LDS, added as
+// first + second, before the scales, biases and SwiGLU.
+// NWS streams per block; the block has NW = NWS·KS wavefronts.
+template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS>
+__global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_skinny(
     ExpertKArgs p) {
+  constexpr int NW = NWS * KS;
+  static_assert(KS == 1 || (KS == 2 && !GROUPED), "K split only with one scale per column");
   // Up with NS = 2: one wavefront streams glu then lin of its column group.
   // Up with NS = 1: glu and lin on paired wavefronts (2w, 2w+1), which meet
   // in LDS after the stream. Down: NS column groups per wavefront.
   constexpr bool PAIRED = MODE == MODE_UP && NS == 1;
-  static_assert(!PAIRED || NW % 2 == 0, "paired up needs an even wavefront count");
+  static_assert(!PAIRED || NWS % 2 == 0, "paired up needs an even stream count");
   constexpr int GPW = (MODE == MODE_UP) ? 1 : NS;  // column groups per wavefront
   constexpr bool SPLIT = AStage<AT>::SPLIT;
   // LDS: the staged A rows, then each wavefront's parked glu sums
@@ -181,10 +188,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
+  const int sw = wave / KS;     // stream of this wavefront
+  const int kpart = wave % KS;  // its half of K when split
   const int N4 = p.N / 4, K4 = p.K / 4;
-  const int arr = PAIRED ? (wave & 1) : 0;  // weight array of a paired wavefront
-  const int cg0 = PAIRED ? blockIdx.x * (NW / 2) + (wave >> 1)
-                         : (blockIdx.x * NW + wave) * GPW;  // first column group
+  const int arr = PAIRED ? (sw & 1) : 0;  // weight array of a paired stream
+  const int cg0 = PAIRED ? blockIdx.x * (NWS / 2) + (sw >> 1)
+                         : (blockIdx.x * NWS + sw) * GPW;  // first column group
   int useg[NS];
   bool uok[NS];
 #pragma unroll
@@ -195,14 +204,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
   const int kq = lane >> 4;
   const int m = lane & 15;
   const int steps = (p.K + 31) / 32;
-  const int gsteps = NS * steps;
+  const int lsteps = steps / KS;  // steps of this wavefront per segment (KS divides steps)
+  const int kbeg = kpart * lsteps;
+  const int gsteps = NS * lsteps;
   const int kg = p.K / p.g;
   const int kp = a_stage_kp(p.K);
   const int RC = p.rc;
   const int planes = SPLIT ? 2 : 1;
   _Float16 *alo = ahi + RC * kp;
-  floatx4 *park = (floatx4 *)(smem + (size_t)RC * kp * 2 * planes) +
-                  (PAIRED ? (wave >> 1) : wave) * 4 * WAVE;
+  floatx4 *park0 = (floatx4 *)(smem + (size_t)RC * kp * 2 * planes);
+  floatx4 *park = park0 + (PAIRED ? (sw >> 1) : sw) * 4 * WAVE;
+  // K-split partial sums, one [4][64] floatx4 slot per stream, after the parks.
+  floatx4 *red = park0 + (MODE == MODE_UP ? (PAIRED ? NWS / 2 : NWS) : 0) * 4 * WAVE +
+                 sw * 4 * WAVE;
 
   // Loaded units: instruction 0 takes unit 16·cg + (lane & 7), instruction 1
   // unit 16·cg + 8 + (lane & 7); tile (lane >> 3) of the step, ^ 1 for
@@ -241,8 +255,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
   // Steps past the stream load zeros (out-of-range offsets), so every
   // phase of the pipeline issues its loads unconditionally.
   auto issue = [&](int g, WStep &d) {
-    const int seg = NS == 1 ? 0 : (g >= steps ? 1 : 0);
-    const int s = g - seg * steps;
+    const int seg = NS == 1 ? 0 : (g >= lsteps ? 1 : 0);
+    const int s = kbeg + g - seg * lsteps;
     const bool live = g < gsteps;
     const int ka = s * 8 + lt, kb = s * 8 + (lt ^ 1);
     const uint32_t o0 = (live && ka < K4) ? wl[seg][0] + (uint32_t)ka * 16u : OOB;
@@ -296,6 +310,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 
     // tot[i][q]: row 4·kq + q of the chunk, column 4·useg + i.
     auto finish = [&](int seg) {
+      if (KS == 2) {
+        // The second half parks its sums; the first adds them (first + second).
+        if (kpart == 1) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) red[i * WAVE + lane] = tot[i];
+        }
+        __syncthreads();
+        if (kpart == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) tot[i] = tot[i] + red[i * WAVE + lane];
+        }
+        __syncthreads();
+        if (kpart == 1) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) tot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+          return;
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         if (!GROUPED) tot[i] = tot[i] * sone[seg][i];
@@ -332,8 +364,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     };
 
     auto compute = [&](int g, const WStep &d) {
-      const int seg = NS == 1 ? 0 : (g >= steps ? 1 : 0);
-      const int s = g - seg * steps;
+      const int seg = NS == 1 ? 0 : (g >= lsteps ? 1 : 0);
+      const int s = kbeg + g - seg * lsteps;
       half8 a_hi = a_frag(ahi, kp, ar, s, kq);
       half8 a_lo;
       if (SPLIT) a_lo = a_frag(alo, kp, ar, s, kq);
@@ -366,7 +398,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
           }
         }
       }
-      if (s == steps - 1) finish(seg);
+      if (s == kbeg + lsteps - 1) finish(seg);
     };
 
     // Buffers rotate b0 → b1 → b2 → b3 (loads three steps ahead). The loads
@@ -383,13 +415,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
       if (g + 3 < gsteps) compute(g + 3, b3);
     }
     if (PAIRED) {
-      // lin wavefront parks its sums; glu wavefront applies the SwiGLU.
-      if (arr == 1) {
+      // lin wavefront parks its sums; glu wavefront applies the SwiGLU (the
+      // first K half of each when split: it holds the whole sums).
+      if (arr == 1 && kpart == 0) {
 #pragma unroll
         for (int i = 0; i < 4; i++) park[i * WAVE + lane] = tot[i];
       }
       __syncthreads();
-      if (arr == 0 && uok[0]) {
+      if (arr == 0 && kpart == 0 && uok[0]) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const int mm = kq * 4 + q;
@@ -416,9 +449,11 @@ int skinny_rows(int K, bool split, int T) {
   return r < cap ? r : cap;
 }
 
-// LDS bytes of k_expert_skinny: the staged A and (up) the parked glu sums.
-size_t skinny_lds_bytes(int K, bool split, int rc, int parks) {
-  return (size_t)rc * a_stage_kp(K) * 2 * (split ? 2 : 1) + (size_t)parks * 4 * WAVE * sizeof(floatx4);
+// LDS bytes of k_expert_skinny: the staged A, (up) the parked glu sums and
+// (K split) one partial-sum slot per stream.
+size_t skinny_lds_bytes(int K, bool split, int rc, int parks, int reds) {
+  return (size_t)rc * a_stage_kp(K) * 2 * (split ? 2 : 1) +
+         (size_t)(parks + reds) * 4 * WAVE * sizeof(floatx4);
 }
 
 __device__ __forceinline__ int route_expert(const float *route, int64_t a, int k, int E) {
@@ -597,15 +632,30 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     if (MODE == MODE_UP && ns == 1 && nw == 1) nw = 2;  // glu/lin pairs
     const int gpw = (MODE == MODE_UP) ? 1 : ns;
     const int cg_per_block = (MODE == MODE_UP && ns == 1) ? nw / 2 : nw * gpw;
-    dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw);
-    // Up parks one [4][64] floatx4 per wavefront (per pair when paired).
+    // Split K over two wavefronts per stream when the unsplit launch has
+    // only a few wavefronts per CU (few active experts and columns: config 1
+    // measured 628k → 712k tokens/s). At ~7 wavefronts per CU (config 3) the
+    // split measured slower (up 53 → 60 µs): shorter streams pay the per-
+    // wavefront start-up twice.
+    const long streams = (long)ea.calls * max_active *
+                         ((ncg + cg_per_block - 1) / cg_per_block) * nw;
+    const int steps = (ea.K + 31) / 32;
+    int ks = (!grouped && steps % 2 == 0 && streams < 1024) ? 2 : 1;
+    static const int env_ks = getenv("MOE_SKINNY_KS") ? atoi(getenv("MOE_SKINNY_KS")) : 0;
+    if (env_ks == 1 || (env_ks == 2 && !grouped && steps % 2 == 0)) ks = env_ks;
+    dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw * ks);
+    // Up parks one [4][64] floatx4 per stream (per pair when paired).
     const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
-    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks);
-#define SKINNY(AT_, GR_, NW_, NS_)                                                        \
-  hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_>), grid, block, lds, s, q)
+    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, ks == 2 ? nw : 0);
+#define SKINNY(AT_, GR_, NW_, NS_, KS_)                                                   \
+  hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_, KS_>), grid, block, lds, s, q)
+#define SKINNY_KS(AT_, GR_, NW_, NS_)                                                     \
+  if constexpr (!GR_) {                                                                   \
+    if (ks == 2) { SKINNY(AT_, GR_, NW_, NS_, 2); } else { SKINNY(AT_, GR_, NW_, NS_, 1); } \
+  } else { SKINNY(AT_, GR_, NW_, NS_, 1); }
 #define SKINNY_NS(AT_, GR_, NW_)                                                          \
-  if (ns == 2) { SKINNY(AT_, GR_, NW_, 2); }                                              \
-  else if constexpr (MODE == MODE_DOWN || NW_ % 2 == 0) { SKINNY(AT_, GR_, NW_, 1); }
+  if (ns == 2) { SKINNY_KS(AT_, GR_, NW_, 2); }                                           \
+  else if constexpr (MODE == MODE_DOWN || NW_ % 2 == 0) { SKINNY_KS(AT_, GR_, NW_, 1); }
 #define SKINNY_NW(AT_, GR_)                                                               \
   if (nw == 1) { SKINNY_NS(AT_, GR_, 1); } else if (nw == 2) { SKINNY_NS(AT_, GR_, 2); }  \
   else { SKINNY_NS(AT_, GR_, 4); }
@@ -616,6 +666,7 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     }
 #undef SKINNY_NW
 #undef SKINNY_NS
+#undef SKINNY_KS
 #undef SKINNY
   } else {
     dim3 grid(ea.A, (ea.N + 255) / 256, ea.calls), block(256);
