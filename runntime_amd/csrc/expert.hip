@@ -161,7 +161,7 @@ __device__ __forceinline__ uint32_t swap8(uint32_t v) {
 // first + second, before the scales, biases and SwiGLU.
 // NWS streams per block; the block has NW = NWS·KS wavefronts.
 template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS>
-__global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_skinny(
+__global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(NS == 1 ? 3 : 4))) void k_expert_skinny(
     ExpertKArgs p) {
   constexpr int NW = NWS * KS;
   static_assert(KS == 1 || (KS == 2 && !GROUPED), "K split only with one scale per column");
@@ -272,22 +272,57 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(4
     issue(1, b1);
     issue(2, b2);
 
-    // Stage this chunk's A rows (gathered through perm) in LDS.
-    for (int r = wave; r < RC; r += NW) {
-      const bool ok = r < rows;
-      const int64_t src = ok ? perm[p0 + c0 + r] / p.a_row_div : 0;
-      const AT *xr = abase + src * p.K;
-      for (int k = lane * 4; k < kp; k += WAVE * 4) {
-        half4 h, l;
+    // Stage this chunk's A rows (gathered through perm) in LDS. Each thread
+    // moves 16-byte pieces (8 halves or 4 floats), 8 pieces in flight at
+    // once; each wavefront reads the rows' sources once (lane r: row r) and
+    // passes them by shuffle. (Loading element by element, one row at a time,
+    // cost several memory latencies per block before the weights streamed.)
+    {
+      constexpr int EPC = 16 / (int)sizeof(AT);  // elements per piece
+      constexpr int NT = 64 * NW;
+      const int cpr = kp / EPC;  // pieces per staged row (kp is a multiple of 8)
+      const int total = RC * cpr;
+      const int srcv = lane < rows ? perm[p0 + c0 + lane] / p.a_row_div : 0;
+      const bool vec = p.K % EPC == 0 && (((uintptr_t)abase) & 15) == 0;
+      for (int b0 = threadIdx.x; b0 < total; b0 += 8 * NT) {
+        u32x4 v[8];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float v = (ok && k + j < p.K) ? (float)xr[k + j] : 0.f;
-          const _Float16 hv = (_Float16)v;
-          h[j] = hv;
-          l[j] = (_Float16)(v - (float)hv);
+        for (int u = 0; u < 8; u++) {
+          const int c = b0 + u * NT;
+          const int r = c < total ? c / cpr : 0;
+          const int k = (c - r * cpr) * EPC;
+          const int src = __shfl(srcv, r);
+          const bool ok = c < total && r < rows;
+          const AT *xr = abase + (int64_t)src * p.K;
+          if (vec) {
+            v[u] = (ok && k < p.K) ? *(const u32x4 *)(xr + k) : u32x4{0, 0, 0, 0};
+          } else {
+            AT e[EPC];
+#pragma unroll
+            for (int j = 0; j < EPC; j++) e[j] = (ok && k + j < p.K) ? xr[k + j] : (AT)0;
+            v[u] = __builtin_bit_cast(u32x4, e);
+          }
         }
-        *(half4 *)(ahi + r * kp + k) = h;
-        if (SPLIT) *(half4 *)(alo + r * kp + k) = l;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int c = b0 + u * NT;
+          if (c >= total) break;
+          const int r = c / cpr, k = (c - r * cpr) * EPC;
+          if constexpr (SPLIT) {
+            const floatx4 f = __builtin_bit_cast(floatx4, v[u]);
+            half4 h, l;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const _Float16 hv = (_Float16)f[j];
+              h[j] = hv;
+              l[j] = (_Float16)(f[j] - (float)hv);
+            }
+            *(half4 *)(ahi + r * kp + k) = h;
+            *(half4 *)(alo + r * kp + k) = l;
+          } else {
+            *(u32x4 *)(ahi + r * kp + k) = v[u];
+          }
+        }
       }
     }
     // Output rows of this lane's sums (rows 4·kq + q of the chunk), fetched
