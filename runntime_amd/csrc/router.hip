@@ -165,8 +165,7 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
 }
 
 // S = ((c_0 + c_1) + c_2) + … + b for the wavefront's experts: the J loads
-// are issued 16 at a time (one memory latency per 16 chunks; the adds wait
-// for them), the adds stay in chunk order.
+// are issued 8 at a time, the adds stay in chunk order.
 template <int NI>
 __device__ __forceinline__ void fold_logits(const float *partial, const float *b, int t, int J,
                                             int E, int lane, float (&vals)[NI]) {
@@ -177,14 +176,15 @@ __device__ __forceinline__ void fold_logits(const float *partial, const float *b
     if (e < E) {
       const float *p = partial + (int64_t)t * J * E + e;
       s = p[0];
-      for (int jj = 1; jj < J; jj += 16) {
-        float v[16];
+      int jj = 1;
+      for (; jj + 8 <= J; jj += 8) {
+        float v[8];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = jj + u < J ? p[(int64_t)(jj + u) * E] : 0.f;
+        for (int u = 0; u < 8; u++) v[u] = p[(int64_t)(jj + u) * E];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-          if (jj + u < J) s = s + v[u];
+        for (int u = 0; u < 8; u++) s = s + v[u];
       }
+      for (; jj < J; jj++) s = s + p[(int64_t)jj * E];
       if (b) s = s + b[e];
     }
     vals[i] = s;
