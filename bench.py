@@ -61,7 +61,8 @@ def layer_flops(cfg):
 # HBM traffic per launch of the roofline kernel, from the committed
 # FETCH_SIZE / WRITE_SIZE counter passes (calibrated against a plain copy);
 # valid for the default launch shape of each workload.
-TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md"}
+TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md",
+                    3: "k_expert_skinny_up_c3_decode_traffic.md"}
 
 
 def profiled_traffic(config, default_shape):
@@ -286,8 +287,9 @@ def main():
         calls = tokens_per_step // cfg.T
     up_ms, up_n = groups.get("up", (0.0, 0))
     up_avg_s = up_ms / max(up_n, 1) / 1e3
-    traffic, traffic_src = profiled_traffic(
-        args.config, args.config != 2 or args.calls_per_launch == 1000)
+    default_shape = ((args.config == 2 and args.calls_per_launch == 1000)
+                     or (args.config == 3 and args.copies == 2) or args.config in (4, 5))
+    traffic, traffic_src = profiled_traffic(args.config, default_shape)
     if args.config in (2, 3):
         per_launch = round(up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1))
         achieved = per_launch / up_avg_s / 1e9
