@@ -189,6 +189,33 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes_per_launch": n * 4, "launches": 4}), flush=True)
 
 
+def gemm_calibration(config):
+    """The vendor library's dense f16 GEMM (torch.matmul → hipBLASLt) at the
+    grouped GEMMs' shapes with every expert's rows stacked: M = T·k, N and K
+    of the up (N = 2·I: glu and lin) and down products. It has no int8
+    conversion, gather, grouping or padding: a practical ceiling for f16 MFMA
+    work of that size on this GPU, reported beside the 2.5 PF peak."""
+    cfg = CONFIGS[config]
+    M = cfg.T * cfg.k
+    res = {}
+    for name, n, k in (("up", 2 * cfg.I, cfg.d), ("down", cfg.d, cfg.I)):
+        a = torch.randn(M, k, device="cuda", dtype=torch.float16)
+        b = torch.randn(k, n, device="cuda", dtype=torch.float16)
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        reps = 20
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            a @ b
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        res[name] = {"M": M, "N": n, "K": k, "ms": round(dt * 1e3, 4),
+                     "tflops": round(2 * M * n * k / dt / 1e12, 1),
+                     "frac_of_peak": round(2 * M * n * k / dt / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    print(json.dumps({"gemm_calibration": cfg.name, "dense_f16_torch_matmul": res}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +232,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
                     help="only run 4 plain device copies of MiB each (reference reading "
                          "for the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--gemm-calibration", action="store_true",
+                    help="only time torch.matmul (hipBLASLt) dense f16 GEMMs of the config's "
+                         "up/down shapes and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -213,6 +243,9 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.gemm_calibration:
+        gemm_calibration(args.config)
         return
     cfg = CONFIGS[args.config]
 
