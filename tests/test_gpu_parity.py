@@ -516,3 +516,68 @@ def test_results_are_ordered_with_torchs_default_stream():
     assert same
     assert torch.equal(first, out.cpu())
     assert first.abs().sum() > 0
+
+
+# ------------------------------------------------- single-token calls
+
+# T = 1 (the decode configs' case): routes with distinct experts, one expert
+# in three slots (three rows of one expert's group), and ids that are not
+# experts.
+ROUTES_T1 = {
+    "distinct": lambda E: [0, 3 % E, 1, E - 1],
+    "duplicate": lambda E: [2 % E, 2 % E, 0, 2 % E],
+    "invalid": lambda E: [1, -1, 3 % E, 1.5],
+}
+
+
+def _route_t1(kind, E):
+    ids = ROUTES_T1[kind](E)
+    return np.array([ids + [0.4, 0.3, 0.2, 0.1]], np.float32)
+
+
+@pytest.mark.parametrize("kind", list(ROUTES_T1))
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+@pytest.mark.parametrize("K,N,E", [(128, 72, 5), (640, 640, 16), (1408, 136, 6), (256, 2048, 8)])
+def test_single_token_up(K, N, E, xdtype, kind):
+    say(f"moeUp T=1 {xdtype} K={K} N={N} E={E} {kind}")
+    _check_up(1, K, N, E, K, 8, k=4, xdtype=xdtype, route=_route_t1(kind, E))
+
+
+@pytest.mark.parametrize("kind", list(ROUTES_T1))
+@pytest.mark.parametrize("K,N,E", [(128, 72, 5), (640, 640, 16), (512, 2048, 8), (384, 136, 6)])
+def test_single_token_down(K, N, E, kind):
+    say(f"moeDown T=1 K={K} N={N} E={E} {kind}")
+    _check_down(1, K, N, E, K, 8, k=4, route=_route_t1(kind, E))
+
+
+def test_single_token_batch_on_shared_weights():
+    """160 single-token calls on shared config-2 weights (stride 0): calls
+    0, 77 and 159 against the oracle; every 16th call against its own
+    standalone moe_layer call. (A lone call has few streams and takes the
+    K-split variant, a different summation order: equal to ~1e-6, not bit
+    for bit.)"""
+    cfg = CONFIGS[2]
+    C = 160
+    say(f"moe_layer_batched T=1 calls={C} shared weights")
+    inp = make_inputs(cfg, seed=12, keep_q=True, bias_rand=True)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn((C, 1, cfg.d), generator=g).to(DEV)
+    res = torch.randn((C, 1, cfg.d), generator=g).to(DEV)
+    out, route = rt.moe_layer_batched(x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                                      res, cfg.k)
+    out, route = host(out), host(route)
+    pk = {n: ref.pack_ekn(inp.q[n].numpy(), 8) for n in ("glu", "lin", "down")}
+    w = {n: (pk[n], getattr(inp, n).scales.cpu().numpy(), getattr(inp, n).bias.cpu().numpy())
+         for n in ("glu", "lin", "down")}
+    for c in (0, 77, 159):
+        xs = x[c].cpu().numpy()
+        want_route = ref.topk(ref.router_logits(xs, inp.router_w.cpu().numpy(),
+                                                inp.router_b.cpu().numpy()), cfg.k)
+        assert np.array_equal(route[c][:, :cfg.k], want_route[:, :cfg.k])
+        act = ref.moe_up(xs, want_route, w["glu"], w["lin"], 8, cfg.d, cfg.E)
+        want = ref.moe_down(act, want_route, w["down"], res[c].cpu().numpy(), 8, cfg.I, cfg.E)
+        assert_close(out[c], want, what=f"call {c}")
+    for c in range(0, C, 16):
+        o1 = rt.moe_layer(x[c], inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                          res[c], cfg.k)
+        assert_close(host(o1), out[c], atol=1e-5, rtol=1e-5, what=f"call {c} vs its single call")
