@@ -4,6 +4,7 @@ Ops (same names and argument meaning as packages/runntime/src/core):
   topk, moeUp, moeDown, rmsNorm — the reference's graph ops
   router_topk, moe_layer    — the router+topk fusion and the whole layer
   moe_block                 — EagerMoeMlp.forward (pre-norm + layer + residual)
+  load_moe_block, MoeBlock  — one block's weights from the hosted safetensors layout
 Host-side format helpers: pack_quant_w, pack_expert_weights, QuantW,
 QuantExpertWeight. The compute runs in libmoe.so (HIP, gfx950); see
 include/runntime_moe.h for its C ABI.
@@ -11,6 +12,7 @@ include/runntime_moe.h for its C ABI.
 from .errors import RUNNTIME_ERROR_CODES, RunntimeError, is_runntime_error
 from .quantw import (QuantExpertWeight, QuantW, pack_expert_weights, pack_expert_weights_torch,
                      pack_quant_w)
+from .checkpoint import MoeBlock, load_moe_block, save_moe_block
 from .core import (UploadedExpertWeight, dispatch, moe_block, moe_layer, moe_layer_batched,
                    moeDown, moeUp, pack_quant_w_device, rmsNorm, router_topk, topk,
                    upload_expert_weight)
@@ -20,5 +22,5 @@ __all__ = [
     "pack_expert_weights", "pack_expert_weights_torch", "pack_quant_w", "dispatch", "moe_layer",
     "moe_layer_batched", "pack_quant_w_device",
     "moeDown", "moeUp", "router_topk", "topk", "UploadedExpertWeight", "upload_expert_weight",
-    "moe_block", "rmsNorm",
+    "moe_block", "rmsNorm", "MoeBlock", "load_moe_block", "save_moe_block",
 ]
