@@ -21,6 +21,10 @@
  *                                                  kernel src/core/kernels/reduce/rmsNorm.ts
  *   moe_block        the quantized EagerMoeMlp.forward whole: rmsNorm(x) →
  *                    topk(router) → moeUp → moeDown(+x)  src/zoo/privacy-filter/moeMlp.ts:79-121
+ *   moe_matmul_gather matmulGather(a, w, expertIdx, {bias})
+ *                                                  src/core/graph/ops/matmul.ts:180-210,
+ *                                                  kernel src/core/kernels/matmul/matmulGather.ts
+ *   moe_block_float  EagerMoeMlp.forward, float weights  src/zoo/privacy-filter/moeMlp.ts:79-100
  *   moe_weights_upload / _view / _dispose / _release
  *                    a QuantExpertWeight's buffers uploaded and owned by the
  *                    library (Parameter, src/core/nn/module.ts:20-65)
@@ -177,6 +181,26 @@ MOE_API int moe_block(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const void
 MOE_API int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
                         const void *weight, int weight_len, float eps, int group,
                         const void *residual, float scale, void *out);
+/* matmulGather(a, w, expertIdx, {bias}) (src/core/graph/ops/matmul.ts:180-210):
+ * out[i] = a[i]·W[e_i] + bias[e_i], W = rows [e·K, (e+1)·K) of the float
+ * weight w [E·K, N] (row-major), e_i = expert_idx[i] (f32 [M], exact
+ * integers). a [M, K], w, bias [E, N] (or NULL) and out [M, N] share dtype.
+ * N must be divisible by 4. A row whose index is not an expert is zero. */
+MOE_API int moe_matmul_gather(moe_ctx *ctx, const void *a, moe_dtype dtype, const void *w,
+                              const void *bias, const float *expert_idx, int M, int K, int N,
+                              int E, void *out);
+/* EagerMoeMlp.forward for float weights (src/zoo/privacy-filter/moeMlp.ts
+ * :79-100): xn = rmsNorm(x), route = topk(xn·W + b, k), and per slot
+ * swiglu(gather(xn, glu) , gather(xn, lin)) → gather(·, out), weighted by the
+ * gates and summed over the slots, + x. x, norm_w and the expert weights
+ * and biases share dtype (f32 or f16): glu_w, lin_w [E·d, I], out_w [E·I, d]
+ * row-major, biases [E, I] / [E, d] (or NULL); router W f32 [d, E], b [E] or
+ * NULL. Intermediates are f32; out f32 [T, d]. */
+MOE_API int moe_block_float(moe_ctx *ctx, const void *x, moe_dtype dtype, const void *norm_w,
+                            float eps, const float *w_router, const float *b_router,
+                            const void *glu_w, const void *glu_b, const void *lin_w,
+                            const void *lin_b, const void *out_w, const void *out_b, int T, int d,
+                            int I, int E, int k, float *route_out, float *out);
 /* Strides between the calls of moe_layer_batched, in elements of each
  * tensor (u32 words for quantW weights). 0 shares a tensor between calls. */
 typedef struct moe_call_strides {

@@ -160,3 +160,46 @@ def rmsnorm(x, weight, eps, group=None, residual=None, scale=1.0, dtype=np.float
     lib().orc_rmsnorm(_f(x), rows, cols, group, _f(weight), int(np.asarray(weight).size),
                       float(eps), _f(residual), float(scale), out)
     return out.astype(dtype)
+
+
+def matmul_gather_f64(a, w, bias, idx, K):
+    """matmulGatherRef (test/core/kernels/matmul/matmulGather.gpu.test.ts
+    :10-28) in f64: out[i] = a[i]·W[e_i] + bias[e_i], W = rows [e·K,
+    (e+1)·K) of w [E·K, N]. Rows whose index is not an expert are zero."""
+    a = np.asarray(a, np.float64)
+    w = np.asarray(w, np.float64)
+    bias = None if bias is None else np.asarray(bias, np.float64)
+    E = w.shape[0] // K
+    N = w.shape[1]
+    out = np.zeros((a.shape[0], N))
+    for i, f in enumerate(np.asarray(idx, np.float64)):
+        if not (f >= 0 and f < E and float(int(f)) == f):
+            continue
+        e = int(f)
+        out[i] = a[i] @ w[e * K:(e + 1) * K]
+        if bias is not None:
+            out[i] += bias.reshape(E, N)[e]
+    return out
+
+
+def moe_block_float_f64(x, xn, route, glu, lin, down, k):
+    """EagerMoeMlp.forward's float branch (src/zoo/privacy-filter/moeMlp.ts
+    :85-100) in f64 on the normalised rows xn and a route: for each slot,
+    swiglu(gather(xn, glu), gather(xn, lin)) → gather(·, down), weighted by
+    the slot's gate and summed in slot order, + x. glu/lin/down: (w, bias)."""
+    T, d = xn.shape
+    K = d
+    I = glu[0].shape[1]
+    y = np.zeros((T, d))
+    for s in range(k):
+        ids = route[:, s]
+        g = matmul_gather_f64(xn, glu[0], glu[1], ids, K)
+        l_ = matmul_gather_f64(xn, lin[0], lin[1], ids, K)
+        gc = np.minimum(g, 7.0)
+        lc = np.clip(l_, -7.0, 7.0)
+        act = gc / (1.0 + np.exp(-1.702 * gc)) * (lc + 1.0)
+        o = matmul_gather_f64(act, down[0], down[1], ids, I)
+        valid = np.array([f >= 0 and f < down[0].shape[0] // I and float(int(f)) == f
+                          for f in ids])
+        y += np.where(valid[:, None], o * route[:, k + s][:, None], 0.0)
+    return np.asarray(x, np.float64) + y

@@ -23,7 +23,7 @@ EXPORTED = (
     "moe_up", "moe_down", "moe_layer", "moe_dispatch", "moe_prof_enable", "moe_prof_read",
     "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
     "moe_weights_upload", "moe_weights_view", "moe_weights_dispose", "moe_weights_release",
-    "moe_block", "moe_rmsnorm",
+    "moe_block", "moe_rmsnorm", "moe_matmul_gather", "moe_block_float",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine", "norm")
 
@@ -85,6 +85,9 @@ def load() -> ctypes.CDLL:
             "moe_block": ([P, P, I, P, ctypes.c_float, P, P, W, W, W, I, I, I, I, I, I, I, I, P,
                            P], I),
             "moe_rmsnorm": ([P, P, I, I, I, P, I, ctypes.c_float, I, P, ctypes.c_float, P], I),
+            "moe_matmul_gather": ([P, P, I, P, P, P, I, I, I, I, P], I),
+            "moe_block_float": ([P, P, I, P, ctypes.c_float, P, P, P, P, P, P, P, P, I, I, I, I, I,
+                                 P, P], I),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(lib, name)

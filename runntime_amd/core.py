@@ -333,6 +333,79 @@ def moe_block(x, norm_w, eps, router_w, router_b, glu: QuantExpertWeight,
     return (out, route) if return_route else out
 
 
+def matmulGather(a, w, expertIdx, opts) -> torch.Tensor:
+    """Indexed matmul plus bias: out[i] = a[i]·W[e_i] + bias[e_i], W = rows
+    [e·K, (e+1)·K) of w [E·K, N], e_i looked up per row
+    (src/core/graph/ops/matmul.ts:180-210). a, w and bias share one float
+    dtype; expertIdx is f32. The bias must be [E, N] (the reference checks
+    only its dtype, a known bug its test records)."""
+    bias = opts["bias"]
+    m, k, dtype = _want2d("matmulGather", a, ("f32", "f16"))
+    r, n, wdt = _want2d("matmulGather.w", w, ("f32", "f16"))
+    if wdt != dtype:
+        raise ValueError(f"matmulGather: w is {wdt} but a is {dtype}")
+    if n % 4 != 0:
+        raise ValueError(f"matmulGather: n {n} must be divisible by 4")
+    if r % k != 0:
+        raise ValueError(f"matmulGather: w rows {r} not a multiple of K {k}")
+    if _dtype_name(bias) != dtype:
+        raise ValueError(f"matmulGather: bias must be {dtype}, got {_dtype_name(bias)}")
+    e = r // k
+    if bias.numel() != e * n:
+        raise ValueError(f"matmulGather: bias must be [{e}, {n}], got {bias.numel()} elems")
+    if _dtype_name(expertIdx) != "f32" or expertIdx.numel() != m:
+        raise ValueError(f"matmulGather: expertIdx must be f32 with {m} elems, got "
+                         f"{expertIdx.numel()}")
+    dev = _device_of(a, w, bias, expertIdx)
+    out = torch.empty((m, n), dtype=a.dtype, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_matmul_gather(_ctx(dev), a.data_ptr(), _xdtype(a), w.data_ptr(),
+                                     bias.data_ptr(), expertIdx.data_ptr(), m, k, n, e,
+                                     out.data_ptr()))
+    return out
+
+
+def moe_block_float(x, norm_w, eps, router_w, router_b, glu_w, glu_b, lin_w, lin_b, out_w, out_b,
+                    k: int = 4, return_route: bool = False):
+    """EagerMoeMlp.forward for float weights (src/zoo/privacy-filter/
+    moeMlp.ts:79-100): rmsNorm, router + topk, per slot the glu/lin gathers,
+    clamped SwiGLU and the out gather, weighted by the gates and summed, + x.
+    x, norm_w and the expert weights share dtype: glu_w, lin_w [E·d, I],
+    out_w [E·I, d], biases [E, I] / [E, d] or None; router W f32 [d, E].
+    Returns f32 [T, d]."""
+    t, d, dtype = _want2d("moe_block_float", x, ("f32", "f16"))
+    if _dtype_name(norm_w) != dtype or norm_w.numel() != d:
+        raise ValueError(f"rmsNorm: weight must be {dtype} with {d} elems, got "
+                         f"({norm_w.numel()},{_dtype_name(norm_w)})")
+    if not (eps > 0):
+        raise ValueError(f"rmsNorm: eps must be positive, got {eps}")
+    rw = _dims(router_w)
+    if _dtype_name(router_w) != "f32" or len(rw) != 2 or rw[0] != d:
+        raise ValueError(f"moe_block_float: router weight must be f32 [{d}, E]")
+    e = rw[1]
+    rows, i, wdt = _want2d("matmulGather.w", glu_w, ("f32", "f16"))
+    if wdt != dtype:
+        raise ValueError(f"matmulGather: w is {wdt} but a is {dtype}")
+    if rows != e * d:
+        raise ValueError(f"moe_block_float: glu weight must be [{e}·{d}, I], got {rows} rows")
+    for name, wt, shape in (("lin", lin_w, (e * d, i)), ("out", out_w, (e * i, d))):
+        if _dtype_name(wt) != dtype or tuple(wt.shape) != shape:
+            raise ValueError(f"moe_block_float: {name} weight must be {dtype} {list(shape)}")
+    for name, bt, nn_ in (("glu", glu_b, i), ("lin", lin_b, i), ("out", out_b, d)):
+        if bt is not None and (_dtype_name(bt) != dtype or bt.numel() != e * nn_):
+            raise ValueError(f"moe_block_float: {name} bias must be {dtype} [{e}, {nn_}]")
+    dev = _device_of(x, norm_w, router_w, router_b, glu_w, lin_w, out_w, glu_b, lin_b, out_b)
+    route = torch.empty((t, 2 * k), dtype=torch.float32, device=dev)
+    out = torch.empty((t, d), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_block_float(_ctx(dev), x.data_ptr(), _xdtype(x), norm_w.data_ptr(),
+                                   float(eps), router_w.data_ptr(), _ptr(router_b),
+                                   glu_w.data_ptr(), _ptr(glu_b), lin_w.data_ptr(), _ptr(lin_b),
+                                   out_w.data_ptr(), _ptr(out_b), t, d, i, e, k,
+                                   route.data_ptr(), out.data_ptr()))
+    return (out, route) if return_route else out
+
+
 def pack_quant_w_device(ints: torch.Tensor, bits: int = 8) -> QuantW:
     """packQuantW (src/core/weights/quantPack.ts:12-28) on the device for a
     whole layer: `ints` is int8 [E, n, k] (each expert output-first, torch's

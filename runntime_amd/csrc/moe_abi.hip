@@ -596,6 +596,124 @@ extern "C" int moe_block(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const v
                     route_out, out);
 }
 
+extern "C" int moe_matmul_gather(moe_ctx *ctx, const void *a, moe_dtype dtype, const void *w,
+                                 const void *bias, const float *expert_idx, int M, int K, int N,
+                                 int E, void *out) {
+  int rc = check_ctx(ctx, "matmulGather");
+  if (rc) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "matmulGather: dtype must be f32 or f16");
+  REQUIRE(M >= 1 && K >= 1 && N >= 1 && E >= 1, "matmulGather: sizes must be positive");
+  REQUIRE(N % 4 == 0, "matmulGather: n " + S(N) + " must be divisible by 4");
+  REQUIRE(E <= DISPATCH_MAX_E, "matmulGather: more than " + S(DISPATCH_MAX_E) + " experts");
+  REQUIRE(a && w && expert_idx && out, "matmulGather: NULL tensor");
+  LayerWs L;
+  if ((rc = plan_ws(ctx, 1, M, 1, E, (size_t)M * 2, 0, 0, 0, L))) return rc;
+  hipStream_t s = ctx->stream;
+  {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_idx_route(expert_idx, M, L.route, s))) return rc;
+    if ((rc = launch_dispatch(L.route, 0, M, E, 1, 1, TILE_M, L.db, s))) return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_DOWN);
+    // Rows whose index is not an expert stay zero (the reference reads
+    // past w for them).
+    if ((rc = launch_zero((float *)out, (size_t)M * N * (dtype == MOE_F16 ? 2 : 4) / 4, s)))
+      return rc;
+    FloatArgs fa{};
+    fa.a = a;
+    fa.a_row_div = 1;
+    fa.w0 = w;
+    fa.b0 = bias;
+    fa.K = K;
+    fa.N = N;
+    fa.out = out;
+    fa.db = L.db;
+    if ((rc = launch_float_expert(fa, MODE_DOWN, dtype, dtype, dtype, M < E ? M : E, 1, s)))
+      return rc;
+  }
+  return after_launch("matmulGather");
+}
+
+extern "C" int moe_block_float(moe_ctx *ctx, const void *x, moe_dtype dtype, const void *norm_w,
+                               float eps, const float *w_router, const float *b_router,
+                               const void *glu_w, const void *glu_b, const void *lin_w,
+                               const void *lin_b, const void *out_w, const void *out_b, int T,
+                               int d, int I, int E, int k, float *route_out, float *out) {
+  int rc = check_ctx(ctx, "moe_block_float");
+  if (rc) return rc;
+  if ((rc = check_k("moe_block_float", k, E, true))) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "moe_block_float: dtype must be f32 or f16");
+  REQUIRE(T >= 1 && d >= 1 && I >= 1, "moe_block_float: sizes must be positive");
+  REQUIRE(d % 4 == 0 && I % 4 == 0,
+          "moe_block_float: d " + S(d) + " and I " + S(I) + " must be multiples of 4");
+  REQUIRE(E <= ROUTER_MAX_E, "moe_block_float: more than " + S(ROUTER_MAX_E) + " experts");
+  REQUIRE(x && norm_w && w_router && glu_w && lin_w && out_w && out,
+          "moe_block_float: NULL tensor");
+  REQUIRE(eps > 0.f, "moe_block_float: eps must be positive, got " + std::to_string(eps));
+  const int A = T * k;
+  const size_t esize = dtype == MOE_F16 ? 2 : 4;
+  LayerWs L;
+  if ((rc = plan_ws(ctx, 1, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
+                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)A * d, L,
+                    (size_t)T * d * esize)))
+    return rc;
+  float *route = route_out ? route_out : L.route;
+  hipStream_t s = ctx->stream;
+  {
+    ProfScope ps(ctx, PG_NORM);
+    NormArgs na{x, norm_w, nullptr, L.xn, dtype, T, d, d, d, eps, 1.0f};
+    if ((rc = launch_rmsnorm(na, s))) return rc;
+  }
+  bool dispatched = false;
+  {
+    ProfScope ps(ctx, PG_ROUTER);
+    RouterArgs ra{L.xn, dtype, 0, w_router, 0, b_router, 0, route, 0, L.partial, T, d, E, k, 1};
+    if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
+  }
+  if (!dispatched) {
+    ProfScope ps(ctx, PG_DISPATCH);
+    if ((rc = launch_dispatch(route, 0, T, E, k, 1, TILE_M, L.db, s))) return rc;
+  }
+  const int max_active = A < E ? A : E;
+  {
+    ProfScope ps(ctx, PG_UP);
+    FloatArgs fa{};
+    fa.a = L.xn;
+    fa.a_row_div = k;
+    fa.w0 = glu_w;
+    fa.b0 = glu_b;
+    fa.w1 = lin_w;
+    fa.b1 = lin_b;
+    fa.K = d;
+    fa.N = I;
+    fa.out = L.act;
+    fa.db = L.db;
+    if ((rc = launch_float_expert(fa, MODE_UP, dtype, dtype, MOE_F32, max_active, 1, s))) return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_DOWN);
+    FloatArgs fa{};
+    fa.a = L.act;
+    fa.a_row_div = 1;
+    fa.w0 = out_w;
+    fa.b0 = out_b;
+    fa.K = I;
+    fa.N = d;
+    fa.out = L.y;
+    fa.db = L.db;
+    if ((rc = launch_float_expert(fa, MODE_DOWN, MOE_F32, dtype, MOE_F32, max_active, 1, s)))
+      return rc;
+  }
+  {
+    ProfScope ps(ctx, PG_COMBINE);
+    if ((rc = launch_combine(L.y, 0, 1, (int64_t)A * d, route, 0, x, dtype, 0, T, d, E, k, out, 0,
+                             1, s)))
+      return rc;
+  }
+  return after_launch("moe_block_float");
+}
+
 extern "C" int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
                            const void *weight, int weight_len, float eps, int group,
                            const void *residual, float scale, void *out) {

@@ -214,3 +214,24 @@ struct NormArgs {
   float eps, scale;
 };
 int launch_rmsnorm(const NormArgs &a, hipStream_t s);
+
+// Float-weight expert products (float.hip): rows grouped by the dispatch,
+// weights row-major [E·K, N] of f32 or f16, biases [E, N] of the same type
+// (may be NULL). MODE_UP: act = swiglu(a·w0 + b0, a·w1 + b1), f32 out;
+// MODE_DOWN: out = a·w0 + b0. Row r of a is perm / a_row_div; out row is the
+// assignment.
+struct FloatArgs {
+  const void *a;
+  int64_t a_cs;
+  int a_row_div;
+  const void *w0, *b0, *w1, *b1;
+  int64_t w0_cs, b0_cs, w1_cs, b1_cs;
+  int K, N;
+  void *out;
+  int64_t out_cs;
+  DispatchBufs db;
+};
+int launch_float_expert(const FloatArgs &p, int mode, moe_dtype a_dt, moe_dtype w_dt,
+                        moe_dtype o_dt, int max_active, int calls, hipStream_t s);
+// route [M, 2] = {idx[i], 1} for a one-slot gather.
+int launch_idx_route(const float *idx, int M, float *route, hipStream_t s);

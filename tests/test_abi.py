@@ -200,3 +200,19 @@ def test_moe_block_rejects_a_bad_norm_weight():
         rt.moe_block(x, _input([4]), 1e-5, _input([8, 2]), None, GLU, LIN, OUT, 2)
     with pytest.raises(ValueError, match=r"rmsNorm: eps must be positive"):
         rt.moe_block(x, _input([8]), 0.0, _input([8, 2]), None, GLU, LIN, OUT, 2)
+
+
+@pytest.mark.parametrize("case", [
+    dict(w=_input([8, 6]), bias=_input([2, 6]), error=r"matmulGather: n 6 must be divisible by 4"),
+    dict(w=_input([10, 8]), error=r"matmulGather: w rows 10 not a multiple of K 4"),
+    dict(idx=_input([3]), error=r"matmulGather: expertIdx must be f32 with 2 elems, got 3"),
+    dict(w=_input([8, 8]).half(), error=r"matmulGather: w is f16 but a is f32"),
+    dict(bias=_input([2, 8]).half(), error=r"matmulGather: bias must be f32, got f16"),
+    dict(bias=_input([1, 8]), error=r"matmulGather: bias must be \[2, 8\], got 8 elems"),
+])
+def test_matmul_gather_rejects(case):
+    # matmulGather.gpu.test.ts:142-170 and ops/matmul.ts:188-203; the last
+    # case is the [E, N] bias check the reference test marks as a known bug.
+    with pytest.raises(ValueError, match=case["error"]):
+        rt.matmulGather(case.get("a", _input([2, 4])), case.get("w", _input([8, 8])),
+                        case.get("idx", _input([2])), {"bias": case.get("bias", _input([2, 8]))})
