@@ -216,6 +216,58 @@ def gemm_calibration(config):
     print(json.dumps({"gemm_calibration": cfg.name, "dense_f16_torch_matmul": res}), flush=True)
 
 
+def float_block_bench(args):
+    """The float-weight block (moe_block_float) at config 2's layer shape
+    (d = I = 640, E = 128, k = 4) with f16 or f32 expert weights and
+    `--float-tokens` tokens per call: one line with tokens/s and the
+    expert-weight stream rate (the distinct active experts' glu, lin and out
+    weights per call, over the measured time of the gate/up and down
+    launches)."""
+    cfg = CONFIGS[2]
+    dt = torch.float16 if args.float == "f16" else torch.float32
+    T, d, I, E, k = args.float_tokens, cfg.d, cfg.I, cfg.E, cfg.k
+    g = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((T, d), generator=g, device="cuda").to(dt)
+    norm = (1 + 0.1 * torch.randn(d, generator=g, device="cuda")).to(dt)
+    rw = 0.02 * torch.randn((d, E), generator=g, device="cuda")
+    mk = lambda r, c, s: (s * torch.randn((r, c), generator=g, device="cuda")).to(dt)
+    glu, lin, down = mk(E * d, I, d ** -0.5), mk(E * d, I, d ** -0.5), mk(E * I, d, I ** -0.5)
+    gb, lb, db = mk(E, I, 0.1), mk(E, I, 0.1), mk(E, d, 0.1)
+
+    def step():
+        return rt.moe_block_float(x, norm, 1e-5, rw, None, glu, gb, lin, lb, down, db, k=k)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt_s = (time.perf_counter() - t0) / args.steps
+    perf.read(reset=True)
+    perf.enable(True)
+    out, route = rt.moe_block_float(x, norm, 1e-5, rw, None, glu, gb, lin, lb, down, db, k=k,
+                                    return_route=True)
+    torch.cuda.synchronize()
+    groups = perf.read(reset=True)
+    perf.enable(False)
+    active = int(torch.unique(route[:, :k]).numel())
+    esize = 2 if dt == torch.float16 else 4
+    wbytes = active * 3 * d * I * esize
+    up_ms = groups.get("up", (0.0, 1))[0] / max(groups.get("up", (0.0, 1))[1], 1)
+    dn_ms = groups.get("down", (0.0, 1))[0] / max(groups.get("down", (0.0, 1))[1], 1)
+    gbs = wbytes / ((up_ms + dn_ms) / 1e3) / 1e9
+    print(json.dumps({
+        "metric": "float-weight MoE block tokens/s at 1 MI355X", "value": round(T / dt_s, 1),
+        "unit": "tokens/s", "ms_per_step": round(dt_s * 1e3, 4), "dtype": args.float,
+        "config": {"workload": f"float_block_T{T}_d{d}_E{E}_k{k}_I{I}_{args.float}",
+                   "active_experts": active},
+        "kernel_ms": {kk: round(v[0] / max(v[1], 1), 5) for kk, v in groups.items()},
+        "expert_stream": {"bytes": wbytes, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -232,6 +284,10 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
                     help="only run 4 plain device copies of MiB each (reference reading "
                          "for the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--float", choices=["f16", "f32"], default=None,
+                    help="only time the float-weight block (moe_block_float) at config 2's "
+                         "layer shape and exit")
+    ap.add_argument("--float-tokens", type=int, default=32)
     ap.add_argument("--gemm-calibration", action="store_true",
                     help="only time torch.matmul (hipBLASLt) dense f16 GEMMs of the config's "
                          "up/down shapes and exit")
@@ -246,6 +302,9 @@ def main():
         return
     if args.gemm_calibration:
         gemm_calibration(args.config)
+        return
+    if args.float:
+        float_block_bench(args)
         return
     cfg = CONFIGS[args.config]
 

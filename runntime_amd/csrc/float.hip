@@ -20,8 +20,6 @@
 namespace {
 
 constexpr int WAVE = 64;
-constexpr int FW = 4;           // wavefronts per block (K split)
-constexpr int FRC = 4;          // rows per chunk
 constexpr int FCOLS = 4 * WAVE;  // columns per block
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
@@ -54,7 +52,12 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) {
 // MODE_UP: act[a] = swiglu(x·glu[e] + bias_glu[e], x·lin[e] + bias_lin[e]).
 // MODE_DOWN (and the plain gather): out[a] = x·w[e] + bias[e].
 // AT: activation type, WT: weight and bias type, OT: output type.
-template <int MODE, typename AT, typename WT, typename OT>
+// FW wavefronts split K; FRC rows per chunk. Decode (experts with a row or
+// two) runs 8 × 2: twice the wavefronts and loads in flight of 4 × 4, whose
+// larger chunks suit experts with more rows (fewer passes over the weights).
+// FU weight rows per loop iteration are in flight: 8 with 2 rows per chunk,
+// 4 with 4 (where 8 costs more registers than it gains).
+template <int MODE, typename AT, typename WT, typename OT, int FW, int FRC, int FU>
 __global__ __launch_bounds__(FW * WAVE) void k_float_expert(FloatArgs p) {
   constexpr int NS = MODE == MODE_UP ? 2 : 1;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -100,16 +103,16 @@ __global__ __launch_bounds__(FW * WAVE) void k_float_expert(FloatArgs p) {
 #pragma unroll
       for (int r = 0; r < FRC; r++) acc[s][r] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (col_ok) {
-      // Four weight rows per iteration, every load issued before the fmas.
+      // FU weight rows per iteration, every load issued before the fmas.
       int kk = kb;
-      for (; kk + 4 <= ke; kk += 4) {
-        float4 wv[NS][4];
+      for (; kk + FU <= ke; kk += FU) {
+        float4 wv[NS][FU];
 #pragma unroll
         for (int s = 0; s < NS; s++)
 #pragma unroll
-          for (int u = 0; u < 4; u++) wv[s][u] = load4w(w[s] + (int64_t)(kk + u) * p.N);
+          for (int u = 0; u < FU; u++) wv[s][u] = load4w(w[s] + (int64_t)(kk + u) * p.N);
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int u = 0; u < FU; u++)
 #pragma unroll
           for (int r = 0; r < FRC; r++) {
             const float xv = xs[r * p.K + kk + u];
@@ -172,8 +175,8 @@ int launch_idx_route(const float *idx, int M, float *route, hipStream_t s) {
   return 0;
 }
 
-size_t float_expert_lds(int K, int mode) {
-  return (size_t)FRC * K * 4 + (size_t)FW * (mode == MODE_UP ? 2 : 1) * FRC * WAVE * 16;
+size_t float_expert_lds(int K, int mode, int fw, int frc) {
+  return (size_t)frc * K * 4 + (size_t)fw * (mode == MODE_UP ? 2 : 1) * frc * WAVE * 16;
 }
 
 int launch_float_expert(const FloatArgs &p, int mode, moe_dtype a_dt, moe_dtype w_dt,
@@ -184,12 +187,19 @@ int launch_float_expert(const FloatArgs &p, int mode, moe_dtype a_dt, moe_dtype 
   MOE_NONNULL(p.db.perm);
   MOE_NONNULL(p.db.active);
   if (mode == MODE_UP) MOE_NONNULL(p.w1);
-  const size_t lds = float_expert_lds(p.K, mode);
+  // Experts with at most ~2 rows on average (decode): 8 wavefronts × 2 rows.
+  const bool small = (long)p.db.A <= 2l * max_active;
+  const int fw = small ? 8 : 4, frc = small ? 2 : 4;
+  const size_t lds = float_expert_lds(p.K, mode, fw, frc);
   if (lds > 64 * 1024)
     return moe_fail(MOE_INVALID_ARGUMENT, "float expert: K " + std::to_string(p.K) +
                                               " is too long for the 64 KB row stage");
-  dim3 grid((p.N + FCOLS - 1) / FCOLS, max_active, calls), block(FW * WAVE);
-#define FLT(M_, A_, W_, O_) hipLaunchKernelGGL((k_float_expert<M_, A_, W_, O_>), grid, block, lds, s, p)
+  dim3 grid((p.N + FCOLS - 1) / FCOLS, max_active, calls), block(fw * WAVE);
+#define FLT(M_, A_, W_, O_)                                                                   \
+  do {                                                                                        \
+    if (small) hipLaunchKernelGGL((k_float_expert<M_, A_, W_, O_, 8, 2, 8>), grid, block, lds, s, p); \
+    else hipLaunchKernelGGL((k_float_expert<M_, A_, W_, O_, 4, 4, 4>), grid, block, lds, s, p);       \
+  } while (0)
   const bool af = a_dt == MOE_F16, wf = w_dt == MOE_F16, of = o_dt == MOE_F16;
   if (mode == MODE_UP) {
     // act is f32 (the layer keeps its intermediates in f32)
