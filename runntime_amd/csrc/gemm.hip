@@ -65,7 +65,19 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// act between the two products of the fused layer (dispatch order): each
+// f32 value v as its f16 split hi = f16(v), lo = f16(v − hi), per pair of
+// columns n, n + 1 (n even): hi(n), hi(n + 1), lo(n), lo(n + 1), 8 bytes at
+// the f32 pair's place. Up stores exactly where the f32 values would go;
+// down takes its hi and lo operands from dwords 0, 2 and 1, 3 of the
+// 16-byte chunks it reads, with no conversion.
+struct f16pair {
+  _Float16 hi, lo;
+};
 
 constexpr int WAVE = 64;
 constexpr int BM = GEMM_TILE_M;  // 128 rows
@@ -176,17 +188,29 @@ struct Tile {
   int kb;    // first step of the part
 };
 
-template <int MODE, typename AT>
+// OPAIR (up): write act as f16 pairs. AT = f16pair (down): read them.
+template <int MODE, typename AT, bool OPAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_expert_gemm(GemmArgs p) {
   constexpr bool SPLIT = sizeof(AT) == 4;
+  constexpr bool PAIRS = std::is_same_v<AT, f16pair>;
+  // f16 A: each wavefront covers all 128 rows and two of each unit's four
+  // columns (4 × 2 MFMA tiles), so one converted weight fragment feeds four
+  // MFMAs. f32 A (split into hi + lo, whose conversion scales with the row
+  // tiles) keeps 64 rows × four columns (2 × 4 tiles).
+  constexpr bool TALL = !SPLIT;
+  constexpr int RT = TALL ? 4 : 2;  // 32-row MFMA tiles per wavefront
+  constexpr int CT = TALL ? 2 : 4;  // columns of each unit per wavefront
   constexpr int A_BYTES = BM * BK * (int)sizeof(AT);  // 8 or 16 KB
   constexpr int STAGE = W_BYTES + A_BYTES;
   constexpr int STAGES = SPLIT ? 4 : 6;               // 128 or 144 KB
   constexpr int LOADS = SPLIT ? 4 : 3;                // ring loads per lane per step
   constexpr int TILE_LOADS = 2;                       // row map + constants, per lane per tile
-  constexpr int STORES = MODE == MODE_UP ? 16 : 32;   // epilogue stores per lane
+  // epilogue stores per lane
+  constexpr int STORES = MODE == MODE_UP ? 8 * RT : 16 * RT;
   constexpr int BASE_WAIT = (STAGES - 2) * LOADS;
+  // vmcnt counts to 63; a smaller count only waits longer (for some stores).
+  constexpr int STORE_WAIT = BASE_WAIT + STORES < 63 ? BASE_WAIT + STORES : 63;
   __shared__ __align__(16) uint8_t lds[STAGES * STAGE];
   __shared__ __align__(16) int32_t rowmap[2][BM];     // assignment of each tile row
   // Per-tile epilogue constants: up → glu scales, lin scales, glu biases,
@@ -211,12 +235,13 @@ void k_expert_gemm(GemmArgs p) {
   const int lane = tid & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform
   // Wavefront w runs on SIMD w % 4. Each SIMD holds one wavefront of each
-  // row half, the second with the unit group mirrored by 2 (SIMD s: unit
-  // groups s and s ^ 2). A tile of at most 64 rows (second row half idle)
-  // or of at most 32 units per source (unit groups 2 and 3 idle, as in the
-  // last N-tile of I = 1408) then leaves every SIMD one busy wavefront
-  // instead of idling two SIMDs.
-  const int wm = wave >> 2, wn = wm ? (wave & 3) ^ 2 : wave & 3;
+  // row half (TALL: of each column pair), the second with the unit group
+  // mirrored by 2 (SIMD s: unit groups s and s ^ 2). A tile of at most 32
+  // units per source (unit groups 2 and 3 idle, as in the last N-tile of
+  // I = 1408), or one of at most 64 rows (second row half idle), then leaves
+  // every SIMD one busy wavefront instead of idling two SIMDs.
+  const int wm = TALL ? 0 : wave >> 2, wc = TALL ? wave >> 2 : 0;
+  const int wn = (wave >> 2) ? (wave & 3) ^ 2 : wave & 3;
   const int lm = lane & 31, h = lane >> 5;
   const int N4 = p.N / 4;
   const int ksteps = p.kpart;  // steps per tile
@@ -335,16 +360,17 @@ void k_expert_gemm(GemmArgs p) {
       dma16(ar, P.aoff[i], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + i) * 1024);
   };
 
-  floatx16 acc[2][4];
+  floatx16 acc[RT][CT];
 
   // Fragment positions. B: this lane's slot (up: glu unit 16·wn + (lm & 15)
   // for lm < 16, the same lin unit for lm ≥ 16; down: slot 32·wn + lm),
-  // tiles 4h + 2kk (+1). A: rows 64·wm + 32i + lm, k 16h + 8kk .. +7.
+  // tiles 4h + 2kk (+1), dwords 2·wc .. of each (TALL). A: rows
+  // 64·wm + 32i + lm, k 16h + 8kk .. +7.
   const int slot = MODE == MODE_UP ? (lm < 16 ? 0 : 64) + 16 * wn + (lm & 15) : 32 * wn + lm;
   const int boff = slot * 128, bsw = sw8(slot);
-  int aoff[2], asw[2];
+  int aoff[RT], asw[RT];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < RT; i++) {
     const int arow = 64 * wm + 32 * i + lm;
     aoff[i] = W_BYTES + arow * BK * (int)sizeof(AT);
     asw[i] = SPLIT ? sw8(arow) : sw4(arow);
@@ -352,17 +378,19 @@ void k_expert_gemm(GemmArgs p) {
 
   // One step's fragments as read from LDS: raw weight tiles and A, per
   // 16-k slice kk.
+  using WV = std::conditional_t<TALL, u32x2, u32x4>;  // this lane's CT dwords of a tile
   struct Frags {
-    u32x4 w[2][2];                 // [kk][tile]
-    u32x4 a[2][2][SPLIT ? 2 : 1];  // [kk][i][16-byte chunk]
+    WV w[2][2];                     // [kk][tile]
+    u32x4 a[2][RT][SPLIT ? 2 : 1];  // [kk][i][16-byte chunk]
   };
+  const int wdw = TALL ? 8 * wc : 0;  // byte of the first dword within a tile
   auto read_frags = [&](Frags &F, int stage, int kk) {
     const uint8_t *st = lds + stage * STAGE;
     const int t0 = 4 * h + 2 * kk;
-    F.w[kk][0] = *(const u32x4 *)(st + boff + ((t0 ^ bsw) * 16));
-    F.w[kk][1] = *(const u32x4 *)(st + boff + (((t0 + 1) ^ bsw) * 16));
+    F.w[kk][0] = *(const WV *)(st + boff + ((t0 ^ bsw) * 16) + wdw);
+    F.w[kk][1] = *(const WV *)(st + boff + (((t0 + 1) ^ bsw) * 16) + wdw);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < RT; i++) {
       if constexpr (SPLIT) {
         F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + ((t0 ^ asw[i]) * 16));
         F.a[kk][i][1] = *(const u32x4 *)(st + aoff[i] + (((t0 + 1) ^ asw[i]) * 16));
@@ -375,10 +403,14 @@ void k_expert_gemm(GemmArgs p) {
   // overlaps the MFMAs of column c.
   auto mfma_slice = [&](const Frags &F, int kk) {
     constexpr int PL = SPLIT ? 2 : 1;
-    half8 af[2][PL];
+    half8 af[RT][PL];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if constexpr (SPLIT) {
+    for (int i = 0; i < RT; i++) {
+      if constexpr (PAIRS) {
+        const u32x4 c0 = F.a[kk][i][0], c1 = F.a[kk][i][1];
+        af[i][0] = __builtin_bit_cast(half8, u32x4{c0[0], c0[2], c1[0], c1[2]});
+        af[i][1] = __builtin_bit_cast(half8, u32x4{c0[1], c0[3], c1[1], c1[3]});
+      } else if constexpr (SPLIT) {
         const floatx4 v0 = __builtin_bit_cast(floatx4, F.a[kk][i][0]);
         const floatx4 v1 = __builtin_bit_cast(floatx4, F.a[kk][i][1]);
 #pragma unroll
@@ -393,18 +425,18 @@ void k_expert_gemm(GemmArgs p) {
       }
     }
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int c = 0; c < CT; c++) {
       const half8 bf = cvt_i8x8(F.w[kk][0][c], F.w[kk][1][c]);
 #pragma unroll
       for (int pl = 0; pl < PL; pl++)
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < RT; i++)
           acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][pl], bf, acc[i][c], 0, 0, 0);
     }
   };
 
   // ---- epilogue of tile T from LDS buffer `sel`. acc[i][c][r]: row
-  // 64wm + 32i + 8(r/4) + 4h + r%4, column c of this lane's unit. Outputs go
+  // 64wm + 32i + 8(r/4) + 4h + r%4, column 2wc + c of this lane's unit. Outputs go
   // through a buffer store whose offset is out of range for rows past the
   // tile (the store is dropped): no branches, so the stores queue back to
   // back. (Behind a per-row branch the compiler re-waits for every earlier
@@ -416,6 +448,35 @@ void k_expert_gemm(GemmArgs p) {
   auto pick = [](uint32_t m, float x, float y) {
     return __builtin_bit_cast(float, (m & __builtin_bit_cast(uint32_t, x)) |
                                          (~m & __builtin_bit_cast(uint32_t, y)));
+  };
+  // This lane's CT consecutive output columns of one row (offset past the
+  // buffer: dropped).
+  auto store_cols = [&](const float (&v)[CT], uint32_t off) {
+    if constexpr (CT == 4)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__builtin_bit_cast(uint32_t, v[0]),
+                                                   __builtin_bit_cast(uint32_t, v[1]),
+                                                   __builtin_bit_cast(uint32_t, v[2]),
+                                                   __builtin_bit_cast(uint32_t, v[3])},
+                                             orc, off, 0, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, v[0]),
+                                                  __builtin_bit_cast(uint32_t, v[1])},
+                                            orc, off, 0, 0);
+  };
+  // The same as f16 pairs (at the f32 values' offset).
+  auto store_pairs = [&](const float (&v)[CT], uint32_t off) {
+    uint32_t hl[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c += 2) {
+      const _Float16 h0 = (_Float16)v[c], h1 = (_Float16)v[c + 1];
+      hl[c] = __builtin_bit_cast(uint32_t, half2v{h0, h1});
+      hl[c + 1] = __builtin_bit_cast(
+          uint32_t, half2v{(_Float16)(v[c] - (float)h0), (_Float16)(v[c + 1] - (float)h1)});
+    }
+    if constexpr (CT == 4)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{hl[0], hl[1], hl[2], hl[3]}, orc, off, 0, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{hl[0], hl[1]}, orc, off, 0, 0);
   };
   auto epilogue = [&](const Tile &T, int wu, int sel) {
     // Up with sorted rows writes act at the dispatch position.
@@ -438,12 +499,13 @@ void k_expert_gemm(GemmArgs p) {
       const floatx4 sg = *(const floatx4 *)&cs[q], sl = *(const floatx4 *)&cs[256 + q];
       const floatx4 bg = *(const floatx4 *)&cs[512 + q], bl = *(const floatx4 *)&cs[768 + q];
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int r = 0; r < 8; r++) {
-          floatx4 v;
+          float v[CT];
 #pragma unroll
-          for (int c = 0; c < 4; c++) {
+          for (int c = 0; c < CT; c++) {
+            const int cc = 2 * wc + c;
             const float a0 = acc[i][c][r], a8 = acc[i][c][r + 8];
             const float send = pick(lowm, a8, a0);
             // ds_swizzle, bit mode: lane ^ 16 within each 32 lanes.
@@ -451,12 +513,14 @@ void k_expert_gemm(GemmArgs p) {
                 float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
             const float g = pick(lowm, a0, recv);
             const float l = pick(lowm, recv, a8);
-            v[c] = swiglu(g * sg[c] + bg[c], l * sl[c] + bl[c]);
+            v[c] = swiglu(g * sg[cc] + bg[cc], l * sl[cc] + bl[cc]);
           }
           const int rr = low ? r : r + 8;
           const int row = 64 * wm + 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
-                                                 col_ok ? row_off(row, uo) : 0x80000000u, 0, 0);
+          if constexpr (OPAIR)
+            store_pairs(v, col_ok ? row_off(row, uo) + wdw : 0x80000000u);
+          else
+            store_cols(v, col_ok ? row_off(row, uo) + wdw : 0x80000000u);
         }
     } else {
       const int uo = wu + lm;
@@ -467,15 +531,14 @@ void k_expert_gemm(GemmArgs p) {
       const floatx4 bb = *(const floatx4 *)&cs[512 + q] * (T.part == 0 ? 1.f : 0.f);
       const uint32_t pbase = (uint32_t)T.part * (uint32_t)p.part_floats * 4u;
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int row = 64 * wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-          floatx4 v;
+          float v[CT];
 #pragma unroll
-          for (int c = 0; c < 4; c++) v[c] = acc[i][c][r] * sc[c] + bb[c];
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), orc,
-                                                 col_ok ? row_off(row, uo) + pbase : 0x80000000u, 0, 0);
+          for (int c = 0; c < CT; c++) v[c] = acc[i][c][r] * sc[2 * wc + c] + bb[2 * wc + c];
+          store_cols(v, col_ok ? row_off(row, uo) + wdw + pbase : 0x80000000u);
         }
     }
   };
@@ -522,16 +585,16 @@ void k_expert_gemm(GemmArgs p) {
     // Uniform: waves with no unit below N or no row in the tile skip the MFMAs.
     const bool live = wu < N4 && 64 * wm < cur.rows;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < RT; i++)
 #pragma unroll
-      for (int c = 0; c < 4; c++)
+      for (int c = 0; c < CT; c++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][c][r] = 0.f;
     for (int ks = 0; ks < ksteps; ks++) {
       if (live) mfma_slice(f, 0);
       __builtin_amdgcn_sched_barrier(0);
       // ---- mid-step
-      if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(BASE_WAIT + STORES);
+      if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(STORE_WAIT);
       else if (has_next && ks > tile_step && ks <= tile_step + STAGES - 2) WAIT_VMCNT(BASE_WAIT + TILE_LOADS);
       else WAIT_VMCNT(BASE_WAIT);
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's LDS reads done
@@ -648,16 +711,26 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   if (blocks > cus) blocks = cus;
   blocks = (blocks + 7) / 8 * 8;
   dim3 grid((unsigned)blocks), block(512);
+  // Dispatch-order act (the fused layer, both products here) is stored as
+  // f16 pairs: up writes them, down reads them.
+  const bool pairs = ea.dispatch_order != 0;
   if (ea.mode == MODE_UP) {
-    if (ea.a_dtype == MOE_F16)
-      hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16>), grid, block, 0, s, p);
-    else
-      hipLaunchKernelGGL((k_expert_gemm<MODE_UP, float>), grid, block, 0, s, p);
+    if (ea.a_dtype == MOE_F16) {
+      if (pairs) hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16, false>), grid, block, 0, s, p);
+    } else {
+      if (pairs) hipLaunchKernelGGL((k_expert_gemm<MODE_UP, float, true>), grid, block, 0, s, p);
+      else hipLaunchKernelGGL((k_expert_gemm<MODE_UP, float, false>), grid, block, 0, s, p);
+    }
+  } else if (pairs) {
+    if (ea.a_dtype != MOE_F32)
+      return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: dispatch-order act must be f32");
+    hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, f16pair, false>), grid, block, 0, s, p);
   } else {
     if (ea.a_dtype == MOE_F16)
-      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, _Float16>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, _Float16, false>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, float>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, float, false>), grid, block, 0, s, p);
   }
   return 0;
 }
