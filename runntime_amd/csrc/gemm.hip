@@ -42,11 +42,14 @@
 // into the slot just freed, compute. The waits are explicit vmcnt counts:
 // the compiler does not track loads that write LDS.
 //
-// LDS positions are XOR-swizzled so that the 16-byte fragment reads of any
-// 8 or 16 consecutive lanes hit distinct banks. Rows of 128 bytes (a
-// weight slot's 8 tiles, an f32 A row): chunk c of row r at
-// r·128 + ((c ^ sw8(r))·16), sw8(r) = (r ^ (r >> 3)) & 7. Rows of 64 bytes
-// (an f16 A row): r·64 + ((c ^ sw4(r))·16), sw4(r) = ((r >> 1) ^ (r >> 3)) & 3.
+// LDS positions are chosen so that the fragment reads hit distinct banks
+// (SQ_LDS_BANK_CONFLICT reads 0). Rows of 128 bytes (a weight slot's 8
+// tiles, an f32 A row) are XOR-swizzled: chunk c of row r at
+// r·128 + ((c ^ sw8(r))·16), sw8(r) = (r ^ (r >> 3)) & 7. f16 A rows (64
+// bytes) go chunk-major per 16 rows: chunk c of row r at
+// (r / 16)·1024 + c·256 + (r % 16)·16, so the 16 lanes reading one chunk of
+// 16 rows read 256 contiguous bytes (a row-major layout of 64-byte rows
+// costs two passes per read whatever the swizzle).
 // f32 A is split into f16 hi + lo after the read (two MFMAs per product;
 // ~2^-22 relative).
 //
@@ -142,7 +145,11 @@ __device__ __forceinline__ half8 cvt_i8x8(uint32_t x0, uint32_t x1) {
 }
 
 __device__ __forceinline__ int sw8(int r) { return (r ^ (r >> 3)) & 7; }
-__device__ __forceinline__ int sw4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// Weight slots: sw8, with slots 64-127 (up: lin) moved to the other bank
+// groups (bit 0 flipped) when TALL wavefronts read both sources' tiles at
+// the same 8-byte half in one 32-lane group.
+template <bool TALL>
+__device__ __forceinline__ int sw8w(int s) { return sw8(s) ^ (TALL ? (s >> 6) & 1 : 0); }
 
 // One buffer_load_dwordx4 … lds: 16 bytes per lane from rsrc at voff + soff
 // into LDS at lds_addr + 16·lane. Written as asm so that the compiler, which
@@ -234,15 +241,31 @@ void k_expert_gemm(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform
-  // Wavefront w runs on SIMD w % 4. Each SIMD holds one wavefront of each
-  // row half (TALL: of each column pair), the second with the unit group
-  // mirrored by 2 (SIMD s: unit groups s and s ^ 2). A tile of at most 32
-  // units per source (unit groups 2 and 3 idle, as in the last N-tile of
-  // I = 1408), or one of at most 64 rows (second row half idle), then leaves
-  // every SIMD one busy wavefront instead of idling two SIMDs.
-  const int wm = TALL ? 0 : wave >> 2, wc = TALL ? wave >> 2 : 0;
+  // Slots (weight units of the tile; up: 0-63 glu, 64-127 the same lin
+  // units). Two wavefront shapes:
+  //  - TALL: wavefront w takes all 128 rows and 16 slots, up: glu units
+  //    8w .. 8w + 7 and the same lin units, down: slots 16w .. 16w + 15.
+  //    Lane lm = 2σ + b holds slot σ (up: glu for σ < 8, lin for σ ≥ 8),
+  //    columns 2b and 2b + 1. Neighbouring lanes read the two 8-byte
+  //    halves of one 16-byte tile, and the 8 slots of 16 lanes sit in
+  //    distinct bank groups, so each 16 lanes read 128 bytes without a
+  //    bank conflict.
+  //  - otherwise 2 (row halves) × 4 (unit groups), 64 rows and 32 slots
+  //    each, up: glu units 16·wn .. + 15 and the same lin units; lane lm
+  //    holds slot lm (up: glu for lm < 16), all four columns.
+  // Wavefront w runs on SIMD w % 4. A tile with at most 32 units per source
+  // (the last N-tile of I = 1408) idles the upper unit groups; each SIMD
+  // still keeps one busy wavefront: TALL wavefronts w and w + 4 hold unit
+  // groups w and w + 4; otherwise SIMD s holds unit groups s and s ^ 2 (the
+  // second row half mirrored), which also balances a tile of at most 64 rows.
+  const int wm = TALL ? 0 : wave >> 2;
   const int wn = (wave >> 2) ? (wave & 3) ^ 2 : wave & 3;
   const int lm = lane & 31, h = lane >> 5;
+  constexpr int UPW = TALL ? 8 : 16;  // up: units per source per wavefront
+  // The lane's unit within its group (up: within each source) and the first
+  // of its columns.
+  const int usub = TALL ? (MODE == MODE_UP ? (lm >> 1) & 7 : lm >> 1) : (MODE == MODE_UP ? lm & 15 : lm);
+  const int cb = TALL ? 2 * (lm & 1) : 0;
   const int N4 = p.N / 4;
   const int ksteps = p.kpart;  // steps per tile
 
@@ -315,8 +338,8 @@ void k_expert_gemm(GemmArgs p) {
   // 0-3: source 0, 4-7: source 1); lane l: slot + (l >> 3), position l & 7
   // holds tile (l & 7) ^ sw8(slot). A unit past N gets an offset past the
   // expert's slab, which the buffer's range check turns into zeros.
-  // A: f16 → one instruction, rows 16·wave + (l >> 2), position l & 3 holds
-  //    8-half chunk (l & 3) ^ sw4(row); f32 → instructions i = 0, 1, rows
+  // A: f16 → one instruction, lane l: row 16·wave + (l & 15), 8-half chunk
+  //    l >> 4 (chunk-major); f32 → instructions i = 0, 1, rows
   //    16·wave + 8i + (l >> 3), position l & 7 holds 4-float chunk
   //    (l & 7) ^ sw8(row). Rows past the tile's read its last row: MFMA rows
   //    are independent and the epilogue writes none of them.
@@ -332,7 +355,7 @@ void k_expert_gemm(GemmArgs p) {
     for (int i = 0; i < 2; i++) {
       const int slot = 16 * wave + 8 * i + (lane >> 3);
       const int u = (wave < 4 ? T.U0 : T.U1) + (slot & 63);
-      const int tile = (lane & 7) ^ sw8(slot);
+      const int tile = (lane & 7) ^ sw8w<TALL>(slot);
       P.woff[i] = u < N4 ? (uint32_t)u * (uint32_t)p.K * 4u + tile * 16u : 0x80000000u;
     }
 #pragma unroll
@@ -343,10 +366,10 @@ void k_expert_gemm(GemmArgs p) {
                                        : (uint32_t)(rowmap[sel][r] / p.a_row_div);
         P.aoff[i] = srow * (uint32_t)p.K * 4u + ((lane & 7) ^ sw8(r)) * 16u;
       } else {
-        const int r = 16 * wave + (lane >> 2);
+        const int r = 16 * wave + (lane & 15);
         const uint32_t srow = MODE == MODE_DOWN && p.sorted ? (uint32_t)(T.r0 + min(r, T.rows - 1))
                                        : (uint32_t)(rowmap[sel][r] / p.a_row_div);
-        P.aoff[i] = srow * (uint32_t)p.K * 2u + ((lane & 3) ^ sw4(r)) * 16u;
+        P.aoff[i] = srow * (uint32_t)p.K * 2u + (lane >> 4) * 16u;
       }
     }
     return P;
@@ -362,18 +385,19 @@ void k_expert_gemm(GemmArgs p) {
 
   floatx16 acc[RT][CT];
 
-  // Fragment positions. B: this lane's slot (up: glu unit 16·wn + (lm & 15)
-  // for lm < 16, the same lin unit for lm ≥ 16; down: slot 32·wn + lm),
-  // tiles 4h + 2kk (+1), dwords 2·wc .. of each (TALL). A: rows
-  // 64·wm + 32i + lm, k 16h + 8kk .. +7.
-  const int slot = MODE == MODE_UP ? (lm < 16 ? 0 : 64) + 16 * wn + (lm & 15) : 32 * wn + lm;
-  const int boff = slot * 128, bsw = sw8(slot);
+  // Fragment positions. B: this lane's slot, tiles 4h + 2kk (+1), of each
+  // dwords cb .. (TALL: two, else four). A: rows 64·wm + 32i + lm, k
+  // 16h + 8kk .. +7.
+  const int ug = TALL ? wave : wn;  // unit group
+  const int slot = MODE == MODE_UP ? (lm < 16 ? 0 : 64) + UPW * ug + usub
+                                   : (TALL ? 16 * wave : 32 * wn) + usub;
+  const int boff = slot * 128, bsw = sw8w<TALL>(slot);
   int aoff[RT], asw[RT];
 #pragma unroll
   for (int i = 0; i < RT; i++) {
     const int arow = 64 * wm + 32 * i + lm;
-    aoff[i] = W_BYTES + arow * BK * (int)sizeof(AT);
-    asw[i] = SPLIT ? sw8(arow) : sw4(arow);
+    aoff[i] = W_BYTES + (SPLIT ? arow * BK * 4 : (arow >> 4) * 1024 + (arow & 15) * 16);
+    asw[i] = SPLIT ? sw8(arow) : 0;
   }
 
   // One step's fragments as read from LDS: raw weight tiles and A, per
@@ -383,7 +407,7 @@ void k_expert_gemm(GemmArgs p) {
     WV w[2][2];                     // [kk][tile]
     u32x4 a[2][RT][SPLIT ? 2 : 1];  // [kk][i][16-byte chunk]
   };
-  const int wdw = TALL ? 8 * wc : 0;  // byte of the first dword within a tile
+  const int wdw = 4 * cb;  // byte of the first dword within a tile
   auto read_frags = [&](Frags &F, int stage, int kk) {
     const uint8_t *st = lds + stage * STAGE;
     const int t0 = 4 * h + 2 * kk;
@@ -395,7 +419,7 @@ void k_expert_gemm(GemmArgs p) {
         F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + ((t0 ^ asw[i]) * 16));
         F.a[kk][i][1] = *(const u32x4 *)(st + aoff[i] + (((t0 + 1) ^ asw[i]) * 16));
       } else {
-        F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + (((2 * h + kk) ^ asw[i]) * 16));
+        F.a[kk][i][0] = *(const u32x4 *)(st + aoff[i] + (2 * h + kk) * 256);
       }
     }
   };
@@ -436,7 +460,7 @@ void k_expert_gemm(GemmArgs p) {
   };
 
   // ---- epilogue of tile T from LDS buffer `sel`. acc[i][c][r]: row
-  // 64wm + 32i + 8(r/4) + 4h + r%4, column 2wc + c of this lane's unit. Outputs go
+  // 64wm + 32i + 8(r/4) + 4h + r%4, column cb + c of this lane's unit. Outputs go
   // through a buffer store whose offset is out of range for rows past the
   // tile (the store is dropped): no branches, so the stores queue back to
   // back. (Behind a per-row branch the compiler re-waits for every earlier
@@ -487,13 +511,13 @@ void k_expert_gemm(GemmArgs p) {
     };
     const float *cs = consts[sel];
     if (MODE == MODE_UP) {
-      // Lane lm < 16 holds glu and lane lm + 16 lin of unit wu + (lm & 15):
-      // the low lane finishes rows r < 8 and the high lane rows r ≥ 8, each
+      // Lane lm < 16 holds glu and lane lm + 16 lin of unit wu + usub: the
+      // low lane finishes rows r < 8 and the high lane rows r ≥ 8, each
       // receiving the other projection's values for its rows from its
       // partner.
       const bool low = lm < 16;
       const uint32_t lowm = low ? ~0u : 0u;
-      const int uo = wu + (lm & 15);
+      const int uo = wu + usub;
       const bool col_ok = uo < N4;
       const int q = 4 * (uo - T.U0);  // output index within the tile
       const floatx4 sg = *(const floatx4 *)&cs[q], sl = *(const floatx4 *)&cs[256 + q];
@@ -505,7 +529,7 @@ void k_expert_gemm(GemmArgs p) {
           float v[CT];
 #pragma unroll
           for (int c = 0; c < CT; c++) {
-            const int cc = 2 * wc + c;
+            const int cc = cb + c;
             const float a0 = acc[i][c][r], a8 = acc[i][c][r + 8];
             const float send = pick(lowm, a8, a0);
             // ds_swizzle, bit mode: lane ^ 16 within each 32 lanes.
@@ -523,7 +547,7 @@ void k_expert_gemm(GemmArgs p) {
             store_cols(v, col_ok ? row_off(row, uo) + wdw : 0x80000000u);
         }
     } else {
-      const int uo = wu + lm;
+      const int uo = wu + usub;
       const bool col_ok = uo < N4;
       const int q = 4 * (uo - T.U0);
       // The bias goes into part 0 only; every part carries its scale.
@@ -537,7 +561,7 @@ void k_expert_gemm(GemmArgs p) {
           const int row = 64 * wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
           float v[CT];
 #pragma unroll
-          for (int c = 0; c < CT; c++) v[c] = acc[i][c][r] * sc[2 * wc + c] + bb[2 * wc + c];
+          for (int c = 0; c < CT; c++) v[c] = acc[i][c][r] * sc[cb + c] + bb[cb + c];
           store_cols(v, col_ok ? row_off(row, uo) + wdw + pbase : 0x80000000u);
         }
     }
@@ -581,7 +605,10 @@ void k_expert_gemm(GemmArgs p) {
   for (int j = 0; j < ntiles; j++) {
     const bool has_next = j + 1 < ntiles;
     const int sel = j & 1;
-    const int wu = MODE == MODE_UP ? cur.U0 + 16 * wn : (wn < 2 ? cur.U0 : cur.U1) + 32 * (wn & 1);
+    // First unit of the wavefront's group (up: of each source).
+    const int wu = MODE == MODE_UP ? cur.U0 + UPW * ug
+                   : TALL          ? (wave < 4 ? cur.U0 : cur.U1) + 16 * (wave & 3)
+                                   : (wn < 2 ? cur.U0 : cur.U1) + 32 * (wn & 1);
     // Uniform: waves with no unit below N or no row in the tile skip the MFMAs.
     const bool live = wu < N4 && 64 * wm < cur.rows;
 #pragma unroll
