@@ -28,10 +28,27 @@ constexpr int WAVE = 64;
 __device__ __forceinline__ float load_as_f32(const float *p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float load_as_f32(const _Float16 *p, int64_t i) { return (float)p[i]; }
 
-// (v, e) butterfly arg-max over the wavefront; larger v wins, equal v → lower e.
+// (v, e) arg-max over the wavefront; larger v wins, equal v → lower e. The
+// order is total, so every lane ends with the same winner whatever the
+// tree. Within 16 lanes the partners come from DPP (quad xor 1, quad xor
+// 2, half-row mirror, row mirror: register moves, no LDS trip); across the
+// rows from two xor shuffles.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float &v, int &e) {
+  const float ov = __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+  const int oe = __builtin_amdgcn_mov_dpp(e, CTRL, 0xf, 0xf, false);
+  const bool take = (ov > v) || (ov == v && oe < e);
+  v = take ? ov : v;
+  e = take ? oe : e;
+}
 __device__ __forceinline__ void wave_argmax(float &v, int &e) {
+  argmax_dpp<0xB1>(v, e);   // quad_perm [1, 0, 3, 2]
+  argmax_dpp<0x4E>(v, e);   // quad_perm [2, 3, 0, 1]
+  argmax_dpp<0x141>(v, e);  // row_half_mirror
+  argmax_dpp<0x140>(v, e);  // row_mirror
 #pragma unroll
-  for (int m = 1; m < WAVE; m <<= 1) {
+  for (int m = 16; m < WAVE; m <<= 1) {
     float ov = __shfl_xor(v, m);
     int oe = __shfl_xor(e, m);
     bool take = (ov > v) || (ov == v && oe < e);
@@ -77,11 +94,15 @@ __device__ __forceinline__ int wave_topk_route(const float (&vals)[NI], int E, i
       my_id = si;
     }
   }
-  float m = __shfl(my_v, 0);
+  // Lane reads go through readlane (a register read, no LDS trip).
+  auto lane_f = [](float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  };
+  float m = lane_f(my_v, 0);
   float ex = expf(my_v - m);
-  float z = __shfl(ex, 0);
+  float z = lane_f(ex, 0);
 #pragma unroll 1
-  for (int i = 1; i < k; i++) z = z + __shfl(ex, i);
+  for (int i = 1; i < k; i++) z = z + lane_f(ex, i);
   if (lane < k) {
     row[lane] = (float)my_id;
     row[k + lane] = ex / z;
@@ -164,9 +185,11 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   }
 }
 
-// S = ((c_0 + c_1) + c_2) + … + b for the wavefront's experts: the J loads
-// are issued 8 at a time, the adds stay in chunk order.
-template <int NI>
+// S = ((c_0 + c_1) + c_2) + … + b for the wavefront's experts. The
+// partials come from blocks on every XCD, so each batch of loads waits a
+// full memory latency: the loads go out FB at a time (the launch sizes FB
+// to J, up to 32: d ≤ 2048 in one batch), the adds stay in chunk order.
+template <int NI, int FB>
 __device__ __forceinline__ void fold_logits(const float *partial, const float *b, int t, int J,
                                             int E, int lane, float (&vals)[NI]) {
 #pragma unroll
@@ -175,16 +198,14 @@ __device__ __forceinline__ void fold_logits(const float *partial, const float *b
     float s = -INFINITY;
     if (e < E) {
       const float *p = partial + (int64_t)t * J * E + e;
-      s = p[0];
-      int jj = 1;
-      for (; jj + 8 <= J; jj += 8) {
-        float v[8];
+      for (int j0 = 0; j0 < J; j0 += FB) {
+        float v[FB];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = p[(int64_t)(jj + u) * E];
+        for (int u = 0; u < FB; u++) v[u] = p[(int64_t)min(j0 + u, J - 1) * E];  // in bounds
 #pragma unroll
-        for (int u = 0; u < 8; u++) s = s + v[u];
+        for (int u = 0; u < FB; u++)
+          if (j0 + u < J) s = j0 + u == 0 ? v[u] : s + v[u];
       }
-      for (; jj < J; jj++) s = s + p[(int64_t)jj * E];
       if (b) s = s + b[e];
     }
     vals[i] = s;
@@ -192,7 +213,7 @@ __device__ __forceinline__ void fold_logits(const float *partial, const float *b
 }
 
 // One wavefront per token: fold, top-k, route row.
-template <int NI>
+template <int NI, int FB>
 __global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
   const int lane = threadIdx.x & (moe_dev::WAVE - 1);
   const int t = blockIdx.x * (blockDim.x / moe_dev::WAVE) + threadIdx.x / moe_dev::WAVE;
@@ -202,20 +223,23 @@ __global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
   const float *partial = ra.partial + call * ((int64_t)ra.T * J * ra.E);
   const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
   float vals[NI];
-  fold_logits<NI>(partial, b, t, J, ra.E, lane, vals);
+  fold_logits<NI, FB>(partial, b, t, J, ra.E, lane, vals);
   wave_topk_route<NI>(vals, ra.E, ra.k, lane, ra.route + call * ra.route_cs + (int64_t)t * 2 * ra.k);
 }
 
-// Small calls (T <= 16): one block of 16 wavefronts per call does the fold
+// Small calls (T <= 16): one block per call (a wavefront per token, and at
+// least one thread per assignment: 64·max(T, ⌈T·k / 64⌉) threads) does the fold
 // and top-k of every token, then the call's dispatch (dispatch_dev.h) from
-// the ids it just chose — no second pass over the route.
-template <int NI>
+// the ids it just chose — no second pass over the route. An assignment's
+// place within its expert is its rank among the earlier assignments with
+// that expert, counted over the ids in LDS (at most 256, read by every
+// thread at once).
+template <int NI, int FB>
 __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs ra, DispatchBufs db,
                                                                     int tile_m) {
-  __shared__ int32_t sid[SMALL_T * MAX_K];
+  __shared__ __align__(16) int32_t sid[SMALL_T * MAX_K];
   __shared__ int32_t hist[DISPATCH_MAX_E];
   __shared__ int32_t cursor[DISPATCH_MAX_E + 1];
-  __shared__ int32_t wc[4 * DISPATCH_MAX_E];
   const int lane = threadIdx.x & (moe_dev::WAVE - 1);
   const int t = threadIdx.x / moe_dev::WAVE;
   const int call = blockIdx.x;
@@ -226,7 +250,7 @@ __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs r
     const float *partial = ra.partial + call * ((int64_t)ra.T * J * E);
     const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
     float vals[NI];
-    fold_logits<NI>(partial, b, t, J, E, lane, vals);
+    fold_logits<NI, FB>(partial, b, t, J, E, lane, vals);
     int id = wave_topk_route<NI>(vals, E, k, lane,
                                  ra.route + call * ra.route_cs + (int64_t)t * 2 * k);
     if (lane < k) sid[t * k + lane] = id;
@@ -241,8 +265,19 @@ __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs r
                                db.tile_off + call * db.off_cs(), db.active + call * db.act_cs(),
                                db.meta + call * db.meta_cs(), cursor);
   __syncthreads();
-  int32_t *perm = db.perm + call * db.perm_cs();
-  moe_dev::block_place(e, a, E, cursor, wc, perm);
+  if (e >= 0) {
+    // Four ids per LDS read (the same address for every thread); ids past a
+    // (including the unwritten tail past A) are not counted.
+    const int4 *s4 = (const int4 *)sid;
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < (A + 3) / 4; j++) {
+      const int4 q = s4[j];
+      rank += (4 * j < a && q.x == e) + (4 * j + 1 < a && q.y == e) + (4 * j + 2 < a && q.z == e) +
+              (4 * j + 3 < a && q.w == e);
+    }
+    db.perm[call * db.perm_cs() + cursor[e] + rank] = a;
+  }
 }
 
 // ---------------------------------------- chunk partials for many tokens
@@ -394,16 +429,27 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
       hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, ra);
   }
   const int ni = (ra.E + WAVE - 1) / WAVE;
+  // Fold batch: the chunk count J, rounded up to 8, 16 or 32 (8 with more
+  // than two experts a lane).
+  const int Jc = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const int fb = ni > 2 || Jc <= 8 ? 8 : Jc <= 16 ? 16 : 32;
   if (dispatched) *dispatched = fuse;
   if (fuse) {
+    const int fused_waves = std::max(ra.T, (ra.T * ra.k + WAVE - 1) / WAVE);
+    const int fused_threads = WAVE * fused_waves;  // ≤ 1024: T ≤ 16, k ≤ 16
     MOE_NONNULL(db->offsets);
     MOE_NONNULL(db->perm);
     if (db->E != ra.E || db->A != ra.T * ra.k)
       return moe_fail(MOE_EXECUTION_FAILED, "router: dispatch workspace sized for another shape");
+#define FB_SWITCH(KERNEL, N, GRID, BLOCK, ...)                                                   \
+  do {                                                                                           \
+    if (N > 2 || fb == 8) hipLaunchKernelGGL((KERNEL<N, 8>), GRID, BLOCK, 0, s, __VA_ARGS__);    \
+    else if (fb == 16) hipLaunchKernelGGL((KERNEL<N, 16>), GRID, BLOCK, 0, s, __VA_ARGS__);      \
+    else hipLaunchKernelGGL((KERNEL<N, 32>), GRID, BLOCK, 0, s, __VA_ARGS__);                    \
+  } while (0)
 #define FUSED_NI(N)                                                                        \
   if (ni <= N) {                                                                           \
-    hipLaunchKernelGGL((k_router_fold_topk_dispatch<N>), dim3(ra.calls), dim3(1024), 0, s, ra, \
-                       *db, tile_m);                                                       \
+    FB_SWITCH(k_router_fold_topk_dispatch, N, dim3(ra.calls), dim3(fused_threads), ra, *db, tile_m); \
     return 0;                                                                              \
   }
     FUSED_NI(1) FUSED_NI(2) FUSED_NI(4) FUSED_NI(8)
@@ -412,10 +458,11 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
   dim3 g2((ra.T + 3) / 4, ra.calls);
 #define FOLD_NI(N)                                                                      \
   if (ni <= N) {                                                                        \
-    hipLaunchKernelGGL((k_router_fold_topk<N>), g2, dim3(256), 0, s, ra);               \
+    FB_SWITCH(k_router_fold_topk, N, g2, dim3(256), ra);                                \
     return 0;                                                                           \
   }
   FOLD_NI(1) FOLD_NI(2) FOLD_NI(4) FOLD_NI(8)
 #undef FOLD_NI
+#undef FB_SWITCH
   return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
 }
