@@ -25,6 +25,13 @@
  *                                                  src/core/graph/ops/matmul.ts:180-210,
  *                                                  kernel src/core/kernels/matmul/matmulGather.ts
  *   moe_block_float  EagerMoeMlp.forward, float weights  src/zoo/privacy-filter/moeMlp.ts:79-100
+ *   moe_rope         rope(x, cos, sin, {headDim, srcStart, width})
+ *                                                  src/core/graph/ops/attention.ts:220-262,
+ *                                                  kernel src/core/kernels/attention/rope.ts
+ *   moe_sdpa         sdpa(q, k, v, {qHeads, kvHeads, headDim, windowLeft, windowRight,
+ *                    qPosOffset, sinks, segments, keyBias}) and sdpaPacked (row strides)
+ *                                                  src/core/graph/ops/attention.ts:28-214,
+ *                                                  kernels src/core/kernels/attention/attn*.ts
  *   moe_weights_upload / _view / _dispose / _release
  *                    a QuantExpertWeight's buffers uploaded and owned by the
  *                    library (Parameter, src/core/nn/module.ts:20-65)
@@ -201,6 +208,31 @@ MOE_API int moe_block_float(moe_ctx *ctx, const void *x, moe_dtype dtype, const 
                             const void *glu_w, const void *glu_b, const void *lin_w,
                             const void *lin_b, const void *out_w, const void *out_b, int T, int d,
                             int I, int E, int k, float *route_out, float *out);
+/* rope (src/core/graph/ops/attention.ts:220-262): out [rows, width] =
+ * the interleaved pairs of x's columns [src_start, src_start + width)
+ * rotated by cos/sin (f32 [rows, head_dim], pair-duplicated, any scale
+ * folded in): out[2p] = x0·c − x1·s, out[2p+1] = x1·c + x0·s. x is
+ * [rows, cols] of dtype; out has x's dtype. */
+MOE_API int moe_rope(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
+                     int head_dim, int src_start, int width, const float *cos_t,
+                     const float *sin_t, void *out);
+/* sdpa (src/core/graph/ops/attention.ts:28-145) and sdpaPacked (:146-214,
+ * pass the qkv tensor's q, k and v column blocks with its row stride):
+ * out [q_len, q_heads·head_dim] (dtype) = softmax(q·kᵀ + key bias)·v per
+ * query row i and head h over the keys j with qPos − window_left ≤ j ≤
+ * qPos + window_right (qPos = q_pos_offset + i; a negative window is
+ * unbounded) inside the row's segment [segments[2i], segments[2i+1]) if
+ * given; query head h reads kv head h / (q_heads / kv_heads). q and k
+ * arrive pre-scaled. sinks (f32 [q_heads] or NULL) add exp(sink · ln 2) to
+ * the denominator alone. key_bias adds key_bias_value to the scores of keys
+ * [key_bias_start, key_bias_end). A row that sees no key is 0. Strides are
+ * in elements; head_dim ≤ 128. */
+MOE_API int moe_sdpa(moe_ctx *ctx, moe_dtype dtype, const void *q, int64_t q_stride,
+                     const void *k, int64_t k_stride, const void *v, int64_t v_stride,
+                     int q_len, int kv_len, int q_heads, int kv_heads, int head_dim,
+                     int64_t window_left, int64_t window_right, int q_pos_offset,
+                     const float *sinks, const float *segments, int key_bias,
+                     int key_bias_start, int key_bias_end, float key_bias_value, void *out);
 /* Strides between the calls of moe_layer_batched, in elements of each
  * tensor (u32 words for quantW weights). 0 shares a tensor between calls. */
 typedef struct moe_call_strides {

@@ -203,3 +203,62 @@ def moe_block_float_f64(x, xn, route, glu, lin, down, k):
                           for f in ids])
         y += np.where(valid[:, None], o * route[:, k + s][:, None], 0.0)
     return np.asarray(x, np.float64) + y
+
+
+def rope_f64(x, cos, sin, head_dim, src_start=0, width=None):
+    """ropeRef (test/core/kernels/attention/rope.gpu.test.ts:25-46) in f64:
+    each interleaved pair (x[2p], x[2p+1]) of columns [srcStart, srcStart +
+    width) rotated by the pair-duplicated table entry of its column."""
+    x = np.asarray(x, np.float64)
+    rows, cols = x.shape
+    width = cols if width is None else width
+    c = np.asarray(cos, np.float64).reshape(rows, head_dim)
+    s = np.asarray(sin, np.float64).reshape(rows, head_dim)
+    col = np.arange(0, width, 2)
+    cc, ss = c[:, col % head_dim], s[:, col % head_dim]
+    x0, x1 = x[:, src_start + col], x[:, src_start + col + 1]
+    out = np.empty((rows, width))
+    out[:, 0::2] = x0 * cc - x1 * ss
+    out[:, 1::2] = x1 * cc + x0 * ss
+    return out
+
+
+def sdpa_f64(q, k, v, q_heads, kv_heads, head_dim, window_left=np.inf, window_right=np.inf,
+             q_pos_offset=0, sinks=None, segs=None, key_bias=None):
+    """sdpaRef (test/core/kernels/attention/checkSdpa.ts:55-103) in f64:
+    softmax(q·kᵀ) v per query row and head over the keys the window and the
+    row's segment leave visible; q and k arrive pre-scaled; a sink adds
+    exp(sink · ln 2) to the denominator alone; the key bias (start, end,
+    value) adds value to the scores of its keys; a row that sees no key is
+    0. Vectorised over heads and keys with a mask per row."""
+    q = np.asarray(q, np.float64).reshape(-1, q_heads, head_dim)
+    k = np.asarray(k, np.float64).reshape(-1, kv_heads, head_dim)
+    v = np.asarray(v, np.float64).reshape(-1, kv_heads, head_dim)
+    q_len, kv_len = q.shape[0], k.shape[0]
+    group = q_heads // kv_heads
+    kh = np.repeat(np.arange(kv_heads), group)                 # kv head of each q head
+    scores = np.einsum("ihx,jhx->hij", q, k[:, kh, :])          # [H, qLen, kvLen]
+    if key_bias is not None:
+        s0, e0, val = key_bias
+        scores[:, :, s0:e0] += val
+    j = np.arange(kv_len)
+    out = np.zeros((q_len, q_heads, head_dim))
+    for i in range(q_len):
+        qpos = q_pos_offset + i
+        lo = max(0, qpos - window_left) if np.isfinite(window_left) else 0
+        hi = min(kv_len - 1, qpos + window_right) if np.isfinite(window_right) else kv_len - 1
+        if segs is not None:
+            lo = max(lo, int(segs[2 * i]))
+            hi = min(hi, int(segs[2 * i + 1]) - 1)
+        vis = (j >= lo) & (j <= hi)
+        sc = np.where(vis[None, :], scores[:, i, :], -np.inf)   # [H, kvLen]
+        sink = (np.asarray(sinks, np.float64) * np.log(2.0) if sinks is not None
+                else np.full(q_heads, -np.inf))
+        m = np.maximum(sink, sc.max(axis=1))
+        ok = np.isfinite(m)
+        mm = np.where(ok, m, 0.0)
+        p = np.where(vis[None, :], np.exp(sc - mm[:, None]), 0.0)
+        den = p.sum(axis=1) + np.exp(sink - mm)
+        num = np.einsum("hj,jhx->hx", p, v[:, kh, :])
+        out[i] = np.where(ok[:, None], num / np.where(ok, den, 1.0)[:, None], 0.0)
+    return out.reshape(q_len, q_heads * head_dim)

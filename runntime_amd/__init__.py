@@ -16,7 +16,7 @@ from .quantw import (QuantExpertWeight, QuantW, pack_expert_weights, pack_expert
 from .checkpoint import MoeBlock, load_moe_block, save_moe_block
 from .core import (UploadedExpertWeight, dispatch, matmulGather, moe_block, moe_block_float,
                    moe_layer, moe_layer_batched, moeDown, moeUp, pack_quant_w_device, rmsNorm,
-                   router_topk, topk, upload_expert_weight)
+                   rope, router_topk, sdpa, sdpaPacked, topk, upload_expert_weight)
 
 __all__ = [
     "RUNNTIME_ERROR_CODES", "RunntimeError", "is_runntime_error", "QuantExpertWeight", "QuantW",
@@ -24,5 +24,5 @@ __all__ = [
     "moe_layer_batched", "pack_quant_w_device",
     "moeDown", "moeUp", "router_topk", "topk", "UploadedExpertWeight", "upload_expert_weight",
     "moe_block", "rmsNorm", "MoeBlock", "load_moe_block", "save_moe_block", "matmulGather",
-    "moe_block_float",
+    "moe_block_float", "rope", "sdpa", "sdpaPacked",
 ]

@@ -22,6 +22,8 @@ is 1..16; `topk` takes it, moeUp/moeDown read it from the route's
 import ctypes
 import json
 
+import math
+
 import torch
 
 from . import _lib
@@ -537,3 +539,155 @@ def upload_expert_weight(host_w, scales, bias, E: int, K: int, N: int, bits: int
         sc.ctypes.data if sc.size else None, None if bs is None else bs.ctypes.data,
         E, K, N, bits, group_size, ctypes.byref(out)))
     return UploadedExpertWeight(out.value, E, K, N, bits, group_size)
+
+
+# ------------------------------------------------------------------ attention
+# The attention ops of the privacy-filter block (src/core/graph/ops/
+# attention.ts). WINDOW_INF is the reference's lowering of Infinity
+# (src/core/graph/ops/shared.ts:37); a window at or past it is unbounded.
+WINDOW_INF = 0x3FFFFFFF
+
+
+def rope(x, cos, sin, opts) -> torch.Tensor:
+    """Rotary embedding of the interleaved pairs of x's columns [srcStart,
+    srcStart + width) (src/core/graph/ops/attention.ts:220-262): cos and sin
+    are f32 [T, headDim] pair-duplicated tables with any scale folded in."""
+    head_dim = opts["headDim"]
+    t, xw, dtype = _want2d("rope", x, ("f32", "f16"))
+    src_start = opts.get("srcStart", 0) or 0
+    w = opts.get("width", xw)
+    w = xw if w is None else w
+    if not isinstance(head_dim, int) or head_dim <= 0 or head_dim % 2 != 0:
+        raise ValueError(f"rope: headDim {head_dim} must be a positive even integer")
+    if not isinstance(src_start, int) or src_start < 0 or src_start % 2 != 0:
+        raise ValueError(f"rope: srcStart {src_start} must be a non-negative even integer")
+    if not isinstance(w, int) or w <= 0 or src_start + w > xw:
+        raise ValueError(f"rope: window [{src_start}, {src_start + w}) exceeds {xw} input cols")
+    if w % head_dim != 0:
+        raise ValueError(f"rope: width {w} must be a multiple of headDim {head_dim}")
+    for name, v in (("cos", cos), ("sin", sin)):
+        if _dtype_name(v) != "f32" or v.numel() != t * head_dim:
+            raise ValueError(f"rope: {name} must be f32 [T,headDim] = {t * head_dim} elems, "
+                             f"got {v.numel()}")
+    dev = _device_of(x, cos, sin)
+    out = torch.empty((t, w), dtype=x.dtype, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.moe_rope(_ctx(dev), x.data_ptr(), _xdtype(x), t, xw, head_dim, src_start, w,
+                            cos.data_ptr(), sin.data_ptr(), out.data_ptr()))
+    return out
+
+
+def _lower_window(op, name, w):
+    if w == math.inf:
+        return -1
+    if not isinstance(w, int) or isinstance(w, bool) or w < 0:
+        raise ValueError(f"{op}: {name} {w} must be a non-negative integer or Infinity")
+    return -1 if w >= WINDOW_INF else w
+
+
+def _sdpa_common(op, q_len, kv_len, dtype, opts, packed):
+    q_heads, kv_heads, head_dim = opts["qHeads"], opts["kvHeads"], opts["headDim"]
+    if kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise ValueError(f"{op}: qHeads {q_heads} not divisible by kvHeads {kv_heads}")
+    if head_dim > 128:
+        raise ValueError(f"{op}: headDim {head_dim} exceeds the kernel's max (128)")
+    wl = _lower_window(op, "windowLeft", opts["windowLeft"])
+    wr = _lower_window(op, "windowRight", opts["windowRight"])
+    off = opts.get("qPosOffset", 0) or 0
+    if not isinstance(off, int) or off < 0:
+        raise ValueError(f"{op}: qPosOffset {off} must be a non-negative integer")
+    if wr >= 0 and off + q_len > kv_len:
+        raise ValueError(f"{op}: qPosOffset+qLen {off + q_len} exceeds key rows kvLen {kv_len}")
+    sinks, segments = opts.get("sinks"), opts.get("segments")
+    if sinks is not None and (_dtype_name(sinks) != "f32" or sinks.numel() != q_heads):
+        raise ValueError(f"{op}: sinks must be f32 with {q_heads} elems, got {sinks.numel()}")
+    if segments is not None:
+        if _dtype_name(segments) != "f32" or segments.numel() != 2 * q_len:
+            raise ValueError(f"{op}: segments must be f32 [qLen, 2] = {2 * q_len} elems, got "
+                             f"({segments.numel()},{_dtype_name(segments)})")
+        if q_len == 1 and not packed:
+            raise ValueError(f"{op}: segments need qLen > 1 (decode has no segment route)")
+    max_segment = opts.get("maxSegment", 0) or 0
+    if max_segment != 0:
+        if segments is None:
+            raise ValueError(f"{op}: maxSegment needs segments")
+        if not isinstance(max_segment, int) or max_segment < 1:
+            raise ValueError(f"{op}: maxSegment {max_segment} must be a positive integer")
+    return q_heads, kv_heads, head_dim, wl, wr, off, sinks, segments
+
+
+def _sdpa_launch(dev, q, q_rs, k, k_rs, v, v_rs, q_len, kv_len, q_heads, kv_heads, head_dim, wl,
+                 wr, off, sinks, segments, kb, dtype_t):
+    out = torch.empty((q_len, q_heads * head_dim), dtype=dtype_t, device=dev)
+    lib = _lib.load()
+    kbs, kbe, kbv = (kb["start"], kb["end"], float(kb["value"])) if kb else (0, 0, 0.0)
+    _lib.check(lib.moe_sdpa(_ctx(dev), _xdtype(out), q, q_rs, k, k_rs, v, v_rs, q_len, kv_len,
+                            q_heads, kv_heads, head_dim, wl, wr, off,
+                            sinks.data_ptr() if sinks is not None else None,
+                            segments.data_ptr() if segments is not None else None,
+                            1 if kb else 0, kbs, kbe, kbv, out.data_ptr()))
+    return out
+
+
+def sdpa(q, k, v, opts) -> torch.Tensor:
+    """Scaled-dot-product attention over the band-mask family with GQA,
+    sinks, segments and a key bias (src/core/graph/ops/attention.ts:28-145).
+    q [qLen, qHeads·headDim], k and v [kvLen, kvHeads·headDim] share a float
+    dtype; q and k arrive pre-scaled."""
+    q_len, qw, dtype = _want2d("sdpa", q, ("f32", "f16"))
+    q_heads, head_dim = opts["qHeads"], opts["headDim"]
+    if qw != q_heads * head_dim:
+        raise ValueError(f"sdpa: q cols {qw} != qHeads*headDim {q_heads * head_dim}")
+    kv_heads = opts["kvHeads"]
+    if kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise ValueError(f"sdpa: qHeads {q_heads} not divisible by kvHeads {kv_heads}")
+    kv_len, kw, kdt = _want2d("sdpa.k", k, ("f32", "f16"))
+    if kw != kv_heads * head_dim:
+        raise ValueError(f"sdpa: k cols {kw} != kvHeads*headDim {kv_heads * head_dim}")
+    vt, vw, vdt = _want2d("sdpa.v", v, ("f32", "f16"))
+    if kdt != dtype or vdt != dtype:
+        raise ValueError(f"sdpa: q, k and v must share a dtype, got {dtype}/{kdt}/{vdt}")
+    if vt != kv_len:
+        raise ValueError(f"sdpa: v rows {vt} != k rows {kv_len}")
+    if vw != kv_heads * head_dim:
+        raise ValueError(f"sdpa: v cols {vw} != kvHeads*headDim {kv_heads * head_dim}")
+    q_heads, kv_heads, head_dim, wl, wr, off, sinks, segments = _sdpa_common(
+        "sdpa", q_len, kv_len, dtype, opts, packed=False)
+    kb = opts.get("keyBias")
+    if kb is not None:
+        s0, e0, val = kb["start"], kb["end"], kb["value"]
+        if (not isinstance(s0, int) or not isinstance(e0, int) or s0 < 0 or s0 > e0
+                or e0 > kv_len):
+            raise ValueError(f"sdpa: keyBias keys [{s0}, {e0}) must lie within the {kv_len} keys")
+        if not math.isfinite(val):
+            raise ValueError(f"sdpa: keyBias value {val} must be finite")
+        if q_len == 1:
+            raise ValueError("sdpa: keyBias needs qLen > 1 (decode has no key bias route)")
+    dev = _device_of(q, k, v, *(t for t in (sinks, segments) if t is not None))
+    return _sdpa_launch(dev, q.data_ptr(), qw, k.data_ptr(), kw, v.data_ptr(), vw, q_len, kv_len,
+                        q_heads, kv_heads, head_dim, wl, wr, off, sinks, segments, kb, q.dtype)
+
+
+def sdpaPacked(qkv, opts) -> torch.Tensor:
+    """sdpa over one fused qkv tensor read in place: q, k and v are column
+    blocks of [T, (qHeads + 2·kvHeads)·headDim] (src/core/graph/ops/
+    attention.ts:146-214). Self-attention only."""
+    t, w, dtype = _want2d("sdpaPacked", qkv, ("f32", "f16"))
+    q_heads, kv_heads, head_dim = opts["qHeads"], opts["kvHeads"], opts["headDim"]
+    packed_w = (q_heads + 2 * kv_heads) * head_dim
+    if w != packed_w:
+        raise ValueError(f"sdpaPacked: qkv cols {w} != (qHeads + 2*kvHeads)*headDim = {packed_w}")
+    if kv_heads <= 0 or q_heads % kv_heads != 0:
+        raise ValueError(f"sdpaPacked: qHeads {q_heads} not divisible by kvHeads {kv_heads}")
+    if head_dim > 128:
+        raise ValueError(f"sdpaPacked: headDim {head_dim} exceeds the kernel's max (128)")
+    if t == 1:
+        raise ValueError("sdpaPacked: qLen must be > 1 (decode has no packed route)")
+    q_heads, kv_heads, head_dim, wl, wr, off, sinks, segments = _sdpa_common(
+        "sdpaPacked", t, t, dtype, opts, packed=True)
+    dev = _device_of(qkv, *(x for x in (sinks, segments) if x is not None))
+    es = qkv.element_size()
+    base = qkv.data_ptr()
+    qw, kw = q_heads * head_dim, kv_heads * head_dim
+    return _sdpa_launch(dev, base, w, base + qw * es, w, base + (qw + kw) * es, w, t, t, q_heads,
+                        kv_heads, head_dim, wl, wr, off, sinks, segments, None, qkv.dtype)

@@ -737,6 +737,84 @@ extern "C" int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int row
   return after_launch("rmsNorm");
 }
 
+extern "C" int moe_rope(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
+                        int head_dim, int src_start, int width, const float *cos_t,
+                        const float *sin_t, void *out) {
+  int rc = check_ctx(ctx, "rope");
+  if (rc) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "rope: dtype must be f32 or f16");
+  REQUIRE(rows >= 1 && cols >= 1, "rope: rows and cols must be positive");
+  REQUIRE(head_dim > 0 && head_dim % 2 == 0,
+          "rope: headDim " + S(head_dim) + " must be a positive even integer");
+  REQUIRE(src_start >= 0 && src_start % 2 == 0,
+          "rope: srcStart " + S(src_start) + " must be a non-negative even integer");
+  REQUIRE(width > 0 && (int64_t)src_start + width <= cols,
+          "rope: window [" + S(src_start) + ", " + S(src_start + width) + ") exceeds " + S(cols) +
+              " input cols");
+  REQUIRE(width % head_dim == 0,
+          "rope: width " + S(width) + " must be a multiple of headDim " + S(head_dim));
+  REQUIRE(x && cos_t && sin_t && out, "rope: NULL tensor");
+  if ((rc = launch_rope(x, dtype, rows, cols, head_dim, src_start, width, cos_t, sin_t, out,
+                        ctx->stream)))
+    return rc;
+  return after_launch("rope");
+}
+
+extern "C" int moe_sdpa(moe_ctx *ctx, moe_dtype dtype, const void *q, int64_t q_stride,
+                        const void *k, int64_t k_stride, const void *v, int64_t v_stride,
+                        int q_len, int kv_len, int q_heads, int kv_heads, int head_dim,
+                        int64_t window_left, int64_t window_right, int q_pos_offset,
+                        const float *sinks, const float *segments, int key_bias,
+                        int key_bias_start, int key_bias_end, float key_bias_value, void *out) {
+  int rc = check_ctx(ctx, "sdpa");
+  if (rc) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "sdpa: dtype must be f32 or f16");
+  REQUIRE(q_len >= 1 && kv_len >= 1, "sdpa: qLen and kvLen must be positive");
+  REQUIRE(kv_heads > 0 && q_heads > 0 && q_heads % kv_heads == 0,
+          "sdpa: qHeads " + S(q_heads) + " not divisible by kvHeads " + S(kv_heads));
+  REQUIRE(head_dim >= 1, "sdpa: headDim must be positive");
+  REQUIRE(head_dim <= 128, "sdpa: headDim " + S(head_dim) + " exceeds the kernel's max (128)");
+  REQUIRE(q_pos_offset >= 0,
+          "sdpa: qPosOffset " + S(q_pos_offset) + " must be a non-negative integer");
+  REQUIRE(window_right < 0 || (int64_t)q_pos_offset + q_len <= kv_len,
+          "sdpa: qPosOffset+qLen " + S(q_pos_offset + q_len) + " exceeds key rows kvLen " +
+              S(kv_len));
+  REQUIRE(q_stride >= (int64_t)q_heads * head_dim && k_stride >= (int64_t)kv_heads * head_dim &&
+              v_stride >= (int64_t)kv_heads * head_dim,
+          "sdpa: a row stride is shorter than its heads");
+  if (key_bias)
+    REQUIRE(key_bias_start >= 0 && key_bias_start <= key_bias_end && key_bias_end <= kv_len,
+            "sdpa: keyBias keys [" + S(key_bias_start) + ", " + S(key_bias_end) +
+                ") must lie within the " + S(kv_len) + " keys");
+  REQUIRE(q && k && v && out, "sdpa: NULL tensor");
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_rs = q_stride;
+  a.k_rs = k_stride;
+  a.v_rs = v_stride;
+  a.out = out;
+  a.o_rs = (int64_t)q_heads * head_dim;
+  a.dtype = dtype;
+  a.q_len = q_len;
+  a.kv_len = kv_len;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.window_left = window_left < 0 ? -1 : window_left;
+  a.window_right = window_right < 0 ? -1 : window_right;
+  a.q_pos_offset = q_pos_offset;
+  a.sinks = sinks;
+  a.segs = segments;
+  a.has_kb = key_bias ? 1 : 0;
+  a.kb_start = key_bias_start;
+  a.kb_end = key_bias_end;
+  a.kb_value = key_bias_value;
+  if ((rc = launch_sdpa(a, ctx->stream))) return rc;
+  return after_launch("sdpa");
+}
+
 extern "C" int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const float *w_router,
                          const float *b_router, const moe_expert_weight *glu,
                          const moe_expert_weight *lin, const moe_expert_weight *down,

@@ -217,6 +217,27 @@ struct NormArgs {
 };
 int launch_rmsnorm(const NormArgs &a, hipStream_t s);
 
+// Attention ops (attn.hip). Row strides are in elements; windows < 0 are
+// unbounded; segs f32 [q_len, 2] (first key, end key) or NULL.
+struct AttnArgs {
+  const void *q, *k, *v;
+  int64_t q_rs, k_rs, v_rs;
+  void *out;
+  int64_t o_rs;
+  moe_dtype dtype;
+  int q_len, kv_len, q_heads, kv_heads, head_dim;
+  long long window_left, window_right;
+  int q_pos_offset;
+  const float *sinks;
+  const float *segs;
+  int has_kb, kb_start, kb_end;
+  float kb_value;
+  int rows_per_block;  // set by the launcher
+};
+int launch_rope(const void *x, moe_dtype dt, int rows, int cols, int hd, int src_start, int width,
+                const float *cs, const float *sn, void *out, hipStream_t s);
+int launch_sdpa(AttnArgs a, hipStream_t s);
+
 // Float-weight expert products (float.hip): rows grouped by the dispatch,
 // weights row-major [E·K, N] of f32 or f16, biases [E, N] of the same type
 // (may be NULL). MODE_UP: act = swiglu(a·w0 + b0, a·w1 + b1), f32 out;

@@ -216,3 +216,67 @@ def test_matmul_gather_rejects(case):
     with pytest.raises(ValueError, match=case["error"]):
         rt.matmulGather(case.get("a", _input([2, 4])), case.get("w", _input([8, 8])),
                         case.get("idx", _input([2])), {"bias": case.get("bias", _input([2, 8]))})
+
+
+# ---- attention ops: refusals with the reference's messages
+# (rope.gpu.test.ts:136-177, graph/ops/attention.ts:28-214); they raise
+# before any device work.
+@pytest.mark.parametrize("opts,err", [
+    (dict(headDim=3), r"headDim 3 must be a positive even integer"),
+    (dict(headDim=4, srcStart=1, width=4), r"srcStart 1 must be a non-negative even integer"),
+    (dict(headDim=4, srcStart=8, width=8), r"window \[8, 16\) exceeds 12 input cols"),
+    (dict(headDim=4, width=6), r"width 6 must be a multiple of headDim 4"),
+])
+def test_rope_refusals(opts, err):
+    import runntime_amd as rt
+    x = torch.zeros((2, 12))
+    table = torch.zeros((2, opts["headDim"]))
+    with pytest.raises(ValueError, match=err):
+        rt.rope(x, table, table, opts)
+
+
+def test_rope_refuses_tables_of_the_wrong_size():
+    import runntime_amd as rt
+    x = torch.zeros((2, 8))
+    table = torch.zeros((1, 4))
+    with pytest.raises(ValueError, match=r"cos must be f32 \[T,headDim\] = 8 elems, got 4"):
+        rt.rope(x, table, table, dict(headDim=4))
+
+
+def _sdpa_args(**kw):
+    import math
+    o = dict(qHeads=4, kvHeads=2, headDim=8, windowLeft=math.inf, windowRight=math.inf)
+    o.update(kw)
+    return o
+
+
+@pytest.mark.parametrize("q_cols,opts,err", [
+    (30, _sdpa_args(), r"sdpa: q cols 30 != qHeads\*headDim 32"),
+    (32, _sdpa_args(kvHeads=3), r"sdpa: qHeads 4 not divisible by kvHeads 3"),
+    (32, _sdpa_args(windowLeft=-1), r"sdpa: windowLeft -1 must be a non-negative integer or Infinity"),
+    (32, _sdpa_args(windowRight=1.5), r"sdpa: windowRight 1.5 must be a non-negative integer or Infinity"),
+    (32, _sdpa_args(qPosOffset=-2), r"sdpa: qPosOffset -2 must be a non-negative integer"),
+    (32, _sdpa_args(windowRight=0, qPosOffset=3), r"sdpa: qPosOffset\+qLen 8 exceeds key rows kvLen 5"),
+    (32, _sdpa_args(maxSegment=4), r"sdpa: maxSegment needs segments"),
+])
+def test_sdpa_refusals(q_cols, opts, err):
+    import runntime_amd as rt
+    q = torch.zeros((5, q_cols))
+    k = torch.zeros((5, 16))
+    with pytest.raises(ValueError, match=err):
+        rt.sdpa(q, k, k, opts)
+
+
+def test_sdpa_refuses_mixed_dtypes_and_sinks():
+    import runntime_amd as rt
+    q, k = torch.zeros((5, 32)), torch.zeros((5, 16))
+    with pytest.raises(ValueError, match=r"q, k and v must share a dtype, got f32/f16/f32"):
+        rt.sdpa(q, k.half(), k, _sdpa_args())
+    with pytest.raises(ValueError, match=r"sinks must be f32 with 4 elems, got 3"):
+        rt.sdpa(q, k, k, _sdpa_args(sinks=torch.zeros(3)))
+    with pytest.raises(ValueError, match=r"keyBias keys \[2, 9\) must lie within the 5 keys"):
+        rt.sdpa(q, k, k, _sdpa_args(keyBias=dict(start=2, end=9, value=1.0)))
+    with pytest.raises(ValueError, match=r"sdpaPacked: qkv cols 40 != \(qHeads \+ 2\*kvHeads\)\*headDim = 64"):
+        rt.sdpaPacked(torch.zeros((5, 40)), _sdpa_args())
+    with pytest.raises(ValueError, match=r"sdpaPacked: qLen must be > 1"):
+        rt.sdpaPacked(torch.zeros((1, 64)), _sdpa_args())
