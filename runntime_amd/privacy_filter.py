@@ -1,0 +1,305 @@
+"""The privacy-filter network around the MoE block: YaRN rope tables, the
+attention block, the full block, the model forward, and the host-side
+decoding (log-softmax, constrained Viterbi, token spans).
+
+Reference (src/zoo/privacy-filter/):
+  rope.ts:24-98        computeRopeTables (YaRN: concentration, ramp between
+                       the NTK bounds) and ropeConstants (theta 150000,
+                       scaling 32, ntk α 1 β 32, context 4096; the tables
+                       pair-duplicated and scaled by 64^(−1/4) for q and k)
+  attnBlock.ts:17-57   x + out(sdpa(rope(qkv(norm(x))))): qkv row = q(14×64)
+                       ‖ k(2×64) ‖ v(2×64), window ±128, f32 sinks
+  model.ts:16-76       blocks of attn then MoE, final RMSNorm, unembed
+  config.ts:1-86       the 33 BIOES class names and the label info
+  viterbi.ts:1-148     log-softmax rows and the constrained Viterbi decoder
+  spans.ts:18-70       labels → token spans
+Every device op runs on this library's kernels (rmsNorm, Linear over the
+grouped down product or matmulGather, rope, sdpa, moe_block); the
+embedding table stays on the host as the reference keeps it on the CPU.
+"""
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+from .checkpoint import MoeBlock
+from .linear import Linear
+
+HIDDEN = 640
+QKV_WIDTH = 1152
+ATTN_OUT = 896
+Q_HEADS = 14
+KV_HEADS = 2
+HEAD = 64
+WINDOW = 128
+K_OFF = Q_HEADS * HEAD       # 896
+V_OFF = K_OFF + KV_HEADS * HEAD  # 1024
+RMS_EPS = 1e-5
+QK_SCALE = 0.3535533905932738  # 64^(-1/4), on q and k
+
+
+def compute_rope_tables(positions, head_dim, theta, scaling_factor, ntk_alpha, ntk_beta,
+                        initial_context_length):
+    """YaRN tables (rope.ts:24-63): f32 cos, sin [positions, head_dim / 2]."""
+    half = head_dim // 2
+    freq = theta ** (2.0 * np.arange(half) / head_dim)
+    concentration = 1.0
+    if scaling_factor > 1.0:
+        concentration = 0.1 * math.log(scaling_factor) + 1.0
+        low = half * math.log(initial_context_length / (ntk_beta * 2 * math.pi)) / math.log(theta)
+        high = half * math.log(initial_context_length / (ntk_alpha * 2 * math.pi)) / math.log(theta)
+        ramp = np.clip((np.arange(half) - low) / (high - low), 0.0, 1.0)
+        mask = 1.0 - ramp
+        inv = (1.0 / (scaling_factor * freq)) * (1.0 - mask) + (1.0 / freq) * mask
+    else:
+        inv = 1.0 / freq
+    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
+    return ((np.cos(ang) * concentration).astype(np.float32),
+            (np.sin(ang) * concentration).astype(np.float32))
+
+
+def rope_constants(tokens):
+    """ropeConstants (rope.ts:71-94): pair-duplicated [T, 64] tables with
+    QK_SCALE folded in (the f32 table times QK_SCALE, rounded to f32)."""
+    cos, sin = compute_rope_tables(tokens, HEAD, 150000.0, 32.0, 1.0, 32.0, 4096)
+    cos_e = np.repeat(cos.astype(np.float64) * QK_SCALE, 2, axis=1).astype(np.float32)
+    sin_e = np.repeat(sin.astype(np.float64) * QK_SCALE, 2, axis=1).astype(np.float32)
+    return cos_e, sin_e
+
+
+@dataclass
+class AttnBlock:
+    """EagerAttnBlock (attnBlock.ts:28-57)."""
+    norm_w: torch.Tensor   # [640]
+    qkv: Linear            # 640 → 1152
+    out: Linear            # 896 → 640
+    sinks: torch.Tensor    # f32 [14]
+
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        from .core import _sdpa_launch, rmsNorm, rope
+        t = x.shape[0]
+        qkv = self.qkv.forward(rmsNorm(x, self.norm_w, RMS_EPS))            # [T, 1152] f32
+        q = rope(qkv, cos, sin, {"headDim": HEAD, "srcStart": 0, "width": K_OFF})
+        k = rope(qkv, cos, sin, {"headDim": HEAD, "srcStart": K_OFF, "width": KV_HEADS * HEAD})
+        es = qkv.element_size()
+        attn = _sdpa_launch(qkv.device, q.data_ptr(), K_OFF, k.data_ptr(), KV_HEADS * HEAD,
+                            qkv.data_ptr() + V_OFF * es, QKV_WIDTH, t, t, Q_HEADS, KV_HEADS, HEAD,
+                            WINDOW, WINDOW, 0, self.sinks, None, None, qkv.dtype)
+        return self.out.forward(attn, addend=x)
+
+
+@dataclass
+class Block:
+    """EagerBlock (model.ts:16-33): attention, then the MoE block."""
+    attn: AttnBlock
+    mlp: MoeBlock
+
+    def forward(self, x, cos, sin):
+        return self.mlp.forward(self.attn.forward(x, cos, sin))
+
+
+@dataclass
+class PrivacyFilterModel:
+    """EagerModel (model.ts:44-76): host embedding, blocks, final norm,
+    unembed (no bias) → logits [T, classes]."""
+    embedding: np.ndarray          # [vocab, 640] on the host
+    blocks: List[Block]
+    norm_w: torch.Tensor
+    unembed: Linear
+
+    def forward(self, token_ids) -> torch.Tensor:
+        ids = np.asarray(token_ids, np.int64)
+        dev = self.norm_w.device
+        t = ids.size
+        cos, sin = rope_constants(t)
+        cos_t, sin_t = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        x = torch.from_numpy(np.ascontiguousarray(self.embedding[ids], np.float32)).to(dev)
+        for b in self.blocks:
+            x = b.forward(x, cos_t, sin_t)
+        from .core import rmsNorm
+        return self.unembed.forward(rmsNorm(x, self.norm_w, RMS_EPS))
+
+
+# ------------------------------------------------------------ decoding (host)
+
+V2_SPAN_CLASS_NAMES = ["O", "account_number", "private_address", "private_date", "private_email",
+                       "private_person", "private_phone", "private_url", "secret"]
+V2_NER_CLASS_NAMES = ["O"] + [f"{p}-{base}" for base in V2_SPAN_CLASS_NAMES[1:]
+                              for p in ("B", "I", "E", "S")]
+
+
+@dataclass
+class LabelInfo:
+    span_class_names: List[str]
+    token_to_span_label: dict
+    token_boundary_tags: dict
+    background_token_label: int
+    background_span_label: int
+    num_classes: int
+
+
+def build_label_info(class_names) -> LabelInfo:
+    """buildLabelInfo (config.ts:37-75)."""
+    spans, lookup = ["O"], {"O": 0}
+    to_span, tags, bg = {}, {}, None
+    for idx, name in enumerate(class_names):
+        if name == "O":
+            bg = idx
+            to_span[idx], tags[idx] = 0, None
+            continue
+        dash = name.index("-")
+        tag, base = name[:dash], name[dash + 1:]
+        if base not in lookup:
+            lookup[base] = len(spans)
+            spans.append(base)
+        to_span[idx], tags[idx] = lookup[base], tag
+    if bg is None:
+        raise ValueError("Class names must include 'O'")
+    return LabelInfo(spans, to_span, tags, bg, 0, len(class_names))
+
+
+def log_softmax_rows(logits: np.ndarray) -> np.ndarray:
+    """logSoftmaxRows (viterbi.ts:5-18), per row in f64, stored f32."""
+    x = np.asarray(logits, np.float64)
+    m = x.max(axis=1, keepdims=True)
+    return (x - (np.log(np.exp(x - m).sum(axis=1, keepdims=True)) + m)).astype(np.float32)
+
+
+@dataclass
+class ViterbiBiases:
+    background_stay: float = 0.0
+    background_to_start: float = 0.0
+    inside_to_continue: float = 0.0
+    inside_to_end: float = 0.0
+    end_to_background: float = 0.0
+    end_to_start: float = 0.0
+
+
+class ViterbiDecoder:
+    """The constrained BIOES decoder (viterbi.ts:20-148): start/end scores
+    and a transition matrix of allowed moves (−1e9 elsewhere) with the
+    optional biases; ties keep the lower previous label."""
+    NEG_INF = -1e9
+
+    def __init__(self, info: LabelInfo, biases: Optional[ViterbiBiases] = None):
+        b = biases or ViterbiBiases()
+        n = info.num_classes
+        self.n = n
+        tag = lambda i: info.token_boundary_tags.get(i)
+        span = lambda i: info.token_to_span_label.get(i)
+        is_bg = lambda i: span(i) == info.background_span_label or i == info.background_token_label
+
+        def valid(p, q):
+            q_bg, qt = is_bg(q), tag(q)
+            if (span(q) is None or qt is None) and not q_bg:
+                return False
+            pt = tag(p)
+            if span(p) is None or pt is None or is_bg(p) or pt in ("E", "S"):
+                return q_bg or qt in ("B", "S")
+            if pt in ("B", "I"):
+                return span(p) == span(q) and qt in ("I", "E")
+            return False
+
+        def bias(p, q):
+            pt, qt = tag(p), tag(q)
+            if is_bg(p):
+                if is_bg(q):
+                    return b.background_stay
+                return b.background_to_start if qt in ("B", "S") else 0.0
+            if pt in ("B", "I"):
+                if qt == "I" and span(p) == span(q):
+                    return b.inside_to_continue
+                if qt == "E" and span(p) == span(q):
+                    return b.inside_to_end
+                return 0.0
+            if pt in ("E", "S"):
+                if is_bg(q):
+                    return b.end_to_background
+                return b.end_to_start if qt in ("B", "S") else 0.0
+            return 0.0
+
+        bg = info.background_token_label
+        self.start = np.full(n, self.NEG_INF)
+        self.end = np.full(n, self.NEG_INF)
+        self.trans = np.full((n, n), self.NEG_INF)
+        for i in range(n):
+            t = tag(i)
+            if t in ("B", "S") or i == bg:
+                self.start[i] = 0.0
+            if t in ("E", "S") or i == bg:
+                self.end[i] = 0.0
+            for j in range(n):
+                if valid(i, j):
+                    self.trans[i, j] = bias(i, j)
+
+    def decode(self, log_probs: np.ndarray) -> List[int]:
+        lp = np.asarray(log_probs, np.float32)
+        if lp.ndim != 2 or lp.shape[1] != self.n:
+            raise ValueError(f"Expected width {self.n}, got {lp.shape[-1]}")
+        T = lp.shape[0]
+        if T == 0:
+            return []
+        lp64 = lp.astype(np.float64)
+        scores = lp64[0] + self.start
+        back = np.zeros((max(T - 1, 0), self.n), np.int32)
+        for t in range(1, T):
+            cand = scores[:, None] + self.trans        # [prev, next]
+            best_i = np.argmax(cand, axis=0)            # first maximum: the lower prev
+            back[t - 1] = best_i
+            scores = cand[best_i, np.arange(self.n)] + lp64[t]
+        if not np.isfinite(scores).any():
+            return [int(j) for j in np.argmax(lp, axis=1)]
+        last = int(np.argmax(scores + self.end))
+        path = [0] * T
+        path[T - 1] = last
+        for t in range(T - 2, -1, -1):
+            last = int(back[t, path[t + 1]])
+            path[t] = last
+        return path
+
+
+@dataclass
+class TokenSpan:
+    label: int
+    token_start: int
+    token_end: int  # exclusive
+
+
+def labels_to_spans(labels, info: LabelInfo) -> List[TokenSpan]:
+    """labelsToSpans (spans.ts:18-70)."""
+    spans, cur, start = [], [None], [None]
+
+    def flush(end_excl):
+        if cur[0] is not None and start[0] is not None:
+            spans.append(TokenSpan(cur[0], start[0], end_excl))
+        cur[0], start[0] = None, None
+
+    for idx, lab in enumerate(labels):
+        sl = info.token_to_span_label.get(lab)
+        tag = info.token_boundary_tags.get(lab)
+        if sl is None:
+            continue
+        if sl == info.background_span_label:
+            flush(idx)
+            continue
+        if tag == "S":
+            flush(idx)
+            spans.append(TokenSpan(sl, idx, idx + 1))
+        elif tag == "B":
+            flush(idx)
+            cur[0], start[0] = sl, idx
+        elif tag == "I":
+            if cur[0] is None or cur[0] != sl:
+                flush(idx)
+                cur[0], start[0] = sl, idx
+        elif tag == "E":
+            if cur[0] is None or cur[0] != sl or start[0] is None:
+                flush(idx)
+                spans.append(TokenSpan(sl, idx, idx + 1))
+            else:
+                spans.append(TokenSpan(cur[0], start[0], idx + 1))
+                cur[0], start[0] = None, None
+    flush(len(labels))
+    return spans

@@ -1,0 +1,83 @@
+"""Host-side pieces of the privacy-filter model (runntime_amd/
+privacy_filter.py): the constrained Viterbi decoder against brute force over
+every label path (viterbi.ts:20-148 defines the best-scoring valid path),
+the label info (config.ts:1-75), token spans (spans.ts:18-70), the YaRN
+rope tables at their closed-form limits (rope.ts:24-94) and log-softmax."""
+import itertools
+import math
+
+import numpy as np
+import pytest
+
+from runntime_amd import privacy_filter as pf
+
+
+def test_label_info():
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    assert info.num_classes == 33 and len(info.span_class_names) == 9
+    assert info.background_token_label == 0
+    assert pf.V2_NER_CLASS_NAMES[1:5] == ["B-account_number", "I-account_number",
+                                          "E-account_number", "S-account_number"]
+    assert info.token_boundary_tags[4] == "S" and info.token_to_span_label[4] == 1
+
+
+def _brute(dec, lp):
+    T, n = lp.shape
+    best, arg = -np.inf, None
+    for path in itertools.product(range(n), repeat=T):
+        s = dec.start[path[0]] + lp[0, path[0]] + dec.end[path[-1]]
+        for t in range(1, T):
+            s += dec.trans[path[t - 1], path[t]] + lp[t, path[t]]
+        if s > best:
+            best, arg = s, list(path)
+    return arg
+
+
+@pytest.mark.parametrize("biases", [None, pf.ViterbiBiases(0.3, -0.2, 0.5, -0.1, 0.2, -0.4)])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_viterbi_is_the_best_valid_path(biases, seed):
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info, biases)
+    rng = np.random.default_rng(seed)
+    lp = pf.log_softmax_rows(rng.standard_normal((3, 33)).astype(np.float32) * 3)
+    assert dec.decode(lp) == _brute(dec, lp.astype(np.float64))
+
+
+def test_viterbi_transitions_follow_bioes():
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info)
+    B, I, E, S = 1, 2, 3, 4  # account_number
+    assert dec.trans[0, B] == 0 and dec.trans[0, I] == dec.NEG_INF
+    assert dec.trans[B, I] == 0 and dec.trans[B, E] == 0 and dec.trans[B, 0] == dec.NEG_INF
+    assert dec.trans[B, 6] == dec.NEG_INF  # I of another class
+    assert dec.trans[E, 0] == 0 and dec.trans[S, 5] == 0
+    assert dec.start[I] == dec.NEG_INF and dec.end[B] == dec.NEG_INF
+
+
+def test_labels_to_spans():
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    # O B I E O S, then a dangling I and an E without its B
+    labels = [0, 1, 2, 3, 0, 8, 10, 0, 7]
+    got = [(s.label, s.token_start, s.token_end) for s in pf.labels_to_spans(labels, info)]
+    assert got == [(1, 1, 4), (2, 5, 6), (3, 6, 7), (2, 8, 9)]
+
+
+def test_rope_tables_limits():
+    cos, sin = pf.compute_rope_tables(5, 64, 150000.0, 32.0, 1.0, 32.0, 4096)
+    conc = 0.1 * math.log(32) + 1
+    np.testing.assert_allclose(cos[0], conc, rtol=1e-6)
+    np.testing.assert_array_equal(sin[0], 0)
+    # dims below the ramp keep 1/freq, dims above it 1/(32·freq)
+    freq = 150000.0 ** (2 * np.arange(32) / 64)
+    np.testing.assert_allclose(cos[3, 0], math.cos(3 / freq[0]) * conc, rtol=1e-6)
+    np.testing.assert_allclose(cos[3, 31], math.cos(3 / (32 * freq[31])) * conc, rtol=1e-6)
+    ce, se = pf.rope_constants(5)
+    assert ce.shape == (5, 64)
+    np.testing.assert_array_equal(ce[:, 0], ce[:, 1])
+    np.testing.assert_allclose(ce[0, 0], conc * pf.QK_SCALE, rtol=1e-6)
+
+
+def test_log_softmax_rows():
+    x = np.random.default_rng(0).standard_normal((4, 33)).astype(np.float32)
+    lp = pf.log_softmax_rows(x)
+    np.testing.assert_allclose(np.exp(lp.astype(np.float64)).sum(1), 1, rtol=1e-6)
