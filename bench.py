@@ -268,6 +268,83 @@ def float_block_bench(args):
                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}), flush=True)
 
 
+def privacy_filter_bench(args):
+    """The whole privacy-filter network (8 blocks of attention + the int8
+    MoE block, E = 128, k = 4, d = I = 640, 33 classes) with random int8
+    weights, text in token ids to labelled spans out: embedding gather,
+    forward on the GPU, logits to the host, log-softmax, constrained Viterbi,
+    spans. --pf-texts texts with lengths drawn from 12..100 tokens (the
+    reference's 300 messages of 9-76 words), one text per call; the line
+    reports the median ms per text (the reference's figure: 16.4 ms on an
+    Apple M2 Pro over WebGPU, tokenizer included; none runs here)."""
+    import numpy as np
+    from runntime_amd import privacy_filter as pf
+    from runntime_amd.checkpoint import MoeBlock
+    from runntime_amd.linear import Linear
+    from runntime_amd.quantw import QuantExpertWeight, QuantW
+    rng = np.random.default_rng(0)
+    dev = "cuda"
+    E, k, d, I, vocab = 128, 4, 640, 640, 200064
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    def qlin(out_f, in_f, gs, bias=True):
+        ints = rng.integers(-127, 128, size=(out_f, in_f)).astype(np.int8)
+        sc = (rng.uniform(0.5, 1.5, size=(out_f, in_f // gs)) / (127 * np.sqrt(in_f))).astype(np.float32)
+        return Linear.from_quant(ints, sc, 8, rng.standard_normal(out_f).astype(np.float32) * 0.1
+                                 if bias else None, dev)
+
+    def expert(K, N):
+        q = torch.randint(-127, 128, (E, K, N), generator=g, device=dev, dtype=torch.int8)
+        words = rt.pack_expert_weights_torch(q)
+        return QuantExpertWeight(QuantW(words, (E * K, N)),
+                                 0.5e-3 + 1.5e-3 * torch.rand((E, N), generator=g, device=dev),
+                                 0.01 * torch.randn((E, N), generator=g, device=dev))
+
+    say("building the model (8 blocks, random int8 weights)")
+    blocks = []
+    for _ in range(8):
+        attn = pf.AttnBlock(torch.ones(d, device=dev), qlin(1152, 640, 640), qlin(640, 896, 128),
+                            torch.randn(14, generator=g, device=dev))
+        mlp = MoeBlock(norm_w=torch.ones(d, device=dev),
+                       router_w=0.02 * torch.randn((d, E), generator=g, device=dev), router_b=None,
+                       glu=expert(d, I), lin=expert(d, I), down=expert(I, d), E=E, d=d, I=I,
+                       bits=8, group_up=d, group_down=I, k=k)
+        blocks.append(pf.Block(attn, mlp))
+    emb = rng.standard_normal((vocab, d), dtype=np.float32)
+    model = pf.PrivacyFilterModel(emb, blocks, torch.ones(d, device=dev), qlin(36, 640, 640, False))
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info)
+    lengths = rng.integers(12, 101, size=args.pf_texts)
+    texts = [rng.integers(0, vocab, size=n) for n in lengths]
+
+    def detect(ids):
+        logits = model.forward(ids)[:, :33].cpu().numpy()
+        return pf.labels_to_spans(dec.decode(pf.log_softmax_rows(logits)), info)
+
+    for ids in texts[:max(1, args.warmup)]:
+        detect(ids)
+    torch.cuda.synchronize()
+    times = []
+    t_all = time.perf_counter()
+    for ids in texts:
+        t0 = time.perf_counter()
+        detect(ids)
+        times.append(time.perf_counter() - t0)
+    total = time.perf_counter() - t_all
+    med = float(np.median(times)) * 1e3
+    print(json.dumps({
+        "metric": "privacy filter ms per text (median) at 1 MI355X", "value": round(med, 3),
+        "unit": "ms", "higher_is_better": False, "texts": len(texts),
+        "texts_per_s": round(len(texts) / total, 1), "dtype": "int8 weights, f32 activations",
+        "data": "synthetic (random int8 weights of the model's shapes, random token ids)",
+        "config": {"workload": "privacy_filter_8blocks_E128_k4_d640_I640",
+                   "tokens_per_text": [int(lengths.min()), int(lengths.max())],
+                   "median_tokens": int(np.median(lengths))},
+        "reference_published": {"value": 16.4, "unit": "ms per text (median)",
+                                "hardware": "Apple M2 Pro, WebGPU/Metal, tokenizer included"}}),
+        flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,6 +365,10 @@ def main():
                     help="only time the float-weight block (moe_block_float) at config 2's "
                          "layer shape and exit")
     ap.add_argument("--float-tokens", type=int, default=32)
+    ap.add_argument("--privacy-filter", action="store_true",
+                    help="only time the whole privacy-filter network, text (token ids) to spans, "
+                         "per text, and exit")
+    ap.add_argument("--pf-texts", type=int, default=300)
     ap.add_argument("--gemm-calibration", action="store_true",
                     help="only time torch.matmul (hipBLASLt) dense f16 GEMMs of the config's "
                          "up/down shapes and exit")
@@ -305,6 +386,9 @@ def main():
         return
     if args.float:
         float_block_bench(args)
+        return
+    if args.privacy_filter:
+        privacy_filter_bench(args)
         return
     cfg = CONFIGS[args.config]
 

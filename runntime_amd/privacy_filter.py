@@ -303,3 +303,90 @@ def labels_to_spans(labels, info: LabelInfo) -> List[TokenSpan]:
                 cur[0], start[0] = None, None
     flush(len(labels))
     return spans
+
+
+# ------------------------------------------------------------------ loading
+
+def _linear_from_file(f, name, in_f, out_f, device, bias_name=None):
+    """A Linear from its torch-layout checkpoint weight [out, in]: I8/U8 +
+    F16 `_scale` (quantized) or float (layers.ts:193-217)."""
+    from .errors import RunntimeError
+    if name not in f.names:
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            f"privacy-filter state dict: missing tensor '{name}'")
+    bias = f.array(bias_name).astype(np.float32) if bias_name and bias_name in f.names else None
+    if name in f.quant:
+        qt = f.quant[name]
+        if qt.shape != [out_f, in_f]:
+            raise RunntimeError("CHECKPOINT_MISMATCH",
+                                f"Linear: {name} has shape {qt.shape}, expected torch layout "
+                                f"[{out_f}, {in_f}]")
+        return Linear.from_quant(qt.ints(), qt.scales(), qt.bits, bias, device, name)
+    w = f.array(name)
+    if list(w.shape) != [out_f, in_f]:
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            f"Linear: {name} has shape {list(w.shape)}, expected torch layout "
+                            f"[{out_f}, {in_f}]")
+    return Linear.from_torch_layout(w.astype(np.float32), bias, device)
+
+
+def load_privacy_filter(path: str, device="cuda", blocks: Optional[int] = None,
+                        experts: Optional[int] = None) -> PrivacyFilterModel:
+    """The whole network from an exported privacy-filter file (our parameter
+    names, RMSNorm scales as `scale` or `weight`; detector.ts:25-90,
+    stateDictHooks.ts:80-87): block.{n}.attn.{norm, qkv, out, sinks},
+    block.{n}.mlp.* (load_moe_block), embedding.weight, norm, unembedding."""
+    from .checkpoint import load_moe_block
+    from .errors import RunntimeError
+    from .safetensors import SafetensorsFile
+    f = SafetensorsFile(path)
+    model_meta = f.metadata.get("model") if isinstance(f.metadata, dict) else None
+    if model_meta is not None and model_meta != "privacy-filter":
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            f"privacy-filter weights: file is for model '{model_meta}', expected "
+                            f"'privacy-filter'")
+
+    def norm(prefix):
+        for n in (f"{prefix}.weight", f"{prefix}.scale"):
+            if n in f.names:
+                return torch.from_numpy(f.array(n).astype(np.float32).reshape(-1)).to(device)
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            f"privacy-filter state dict: missing tensor '{prefix}.weight'")
+
+    def need(name):
+        if name not in f.names:
+            raise RunntimeError("CHECKPOINT_MISMATCH",
+                                f"privacy-filter state dict: missing tensor '{name}'")
+        return f.array(name)
+
+    if "embedding.weight" not in f.names:
+        raise RunntimeError("CHECKPOINT_MISMATCH", "privacy-filter weights: missing "
+                            "'embedding.weight' tensor")
+    emb = f.array("embedding.weight").astype(np.float32)
+    if emb.ndim != 2 or emb.shape[1] != HIDDEN:
+        raise RunntimeError("CHECKPOINT_MISMATCH", f"embedding.weight has shape {list(emb.shape)}, "
+                            f"expected [vocab, hidden]")
+    n = 0
+    while f"block.{n}.attn.qkv.weight" in f.names:
+        n += 1
+    if blocks is not None and n != blocks:
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            f"privacy-filter weights: {n} blocks in the file, expected {blocks}")
+    out_blocks = []
+    for b in range(n):
+        p = f"block.{b}.attn"
+        attn = AttnBlock(norm(f"{p}.norm"),
+                         _linear_from_file(f, f"{p}.qkv.weight", HIDDEN, QKV_WIDTH, device,
+                                           f"{p}.qkv.bias"),
+                         _linear_from_file(f, f"{p}.out.weight", ATTN_OUT, HIDDEN, device,
+                                           f"{p}.out.bias"),
+                         torch.from_numpy(need(f"{p}.sinks").astype(np.float32)
+                                          .reshape(-1)).to(device))
+        out_blocks.append(Block(attn, load_moe_block(path, b, device, experts=experts,
+                                                     hidden=HIDDEN)))
+    un = f.infos["unembedding.weight"].shape if "unembedding.weight" in f.names else None
+    if un is None:
+        raise RunntimeError("CHECKPOINT_MISMATCH",
+                            "privacy-filter state dict: missing tensor 'unembedding.weight'")
+    unembed = _linear_from_file(f, "unembedding.weight", HIDDEN, un[0], device)
+    return PrivacyFilterModel(emb, out_blocks, norm("norm"), unembed)
