@@ -317,8 +317,13 @@ def privacy_filter_bench(args):
     lengths = rng.integers(12, 101, size=args.pf_texts)
     texts = [rng.integers(0, vocab, size=n) for n in lengths]
 
+    fwd = model.forward
+    if not args.no_graph:
+        say(f"capturing the forward for {len(set(lengths.tolist()))} text lengths")
+        fwd = pf.GraphedForward(model, lengths.tolist())
+
     def detect(ids):
-        logits = model.forward(ids)[:, :33].cpu().numpy()
+        logits = fwd(ids)[:, :33].cpu().numpy()
         return pf.labels_to_spans(dec.decode(pf.log_softmax_rows(logits)), info)
 
     for ids in texts[:max(1, args.warmup)]:
@@ -339,7 +344,7 @@ def privacy_filter_bench(args):
         "data": "synthetic (random int8 weights of the model's shapes, random token ids)",
         "config": {"workload": "privacy_filter_8blocks_E128_k4_d640_I640",
                    "tokens_per_text": [int(lengths.min()), int(lengths.max())],
-                   "median_tokens": int(np.median(lengths))},
+                   "median_tokens": int(np.median(lengths)), "graph": not args.no_graph},
         "reference_published": {"value": 16.4, "unit": "ms per text (median)",
                                 "hardware": "Apple M2 Pro, WebGPU/Metal, tokenizer included"}}),
         flush=True)

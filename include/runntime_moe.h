@@ -25,6 +25,9 @@
  *                                                  src/core/graph/ops/matmul.ts:180-210,
  *                                                  kernel src/core/kernels/matmul/matmulGather.ts
  *   moe_block_float  EagerMoeMlp.forward, float weights  src/zoo/privacy-filter/moeMlp.ts:79-100
+ *   moe_linear       Linear.forward(x, {addend}) with a float (or load-time dequantized)
+ *                    weight [in, out]             src/core/nn/layers.ts:166-263,
+ *                                                  src/core/graph/compose.ts:45-53
  *   moe_rope         rope(x, cos, sin, {headDim, srcStart, width})
  *                                                  src/core/graph/ops/attention.ts:220-262,
  *                                                  kernel src/core/kernels/attention/rope.ts
@@ -208,6 +211,12 @@ MOE_API int moe_block_float(moe_ctx *ctx, const void *x, moe_dtype dtype, const 
                             const void *glu_w, const void *glu_b, const void *lin_w,
                             const void *lin_b, const void *out_w, const void *out_b, int T, int d,
                             int I, int E, int k, float *route_out, float *out);
+/* Linear (src/core/nn/layers.ts:166-263): out [T, N] = x [T, K] · w [K, N]
+ * + bias [N] (or NULL) + addend [T, N] (or NULL), all f32, w row-major
+ * [in, out] (a quantized checkpoint weight dequantized once at load). Uses
+ * the context workspace for K-slice partial products. */
+MOE_API int moe_linear(moe_ctx *ctx, const float *x, const float *w, const float *bias,
+                       const float *addend, int T, int K, int N, float *out);
 /* rope (src/core/graph/ops/attention.ts:220-262): out [rows, width] =
  * the interleaved pairs of x's columns [src_start, src_start + width)
  * rotated by cos/sin (f32 [rows, head_dim], pair-duplicated, any scale

@@ -179,16 +179,17 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
       for (int i = 0; i < AI; i++) {
         if (!live[i]) continue;
         const float *qr = qs + (wave + AW * i) * HP + sl * 64;
-        float d = s[i];
+        // Two chains (even and odd columns) halve the dependent FMA latency.
+        float d0 = 0.f, d1 = 0.f;
 #pragma unroll
         for (int x = 0; x < 64; x += 4) {
           const float4 t = *(const float4 *)&qr[x];
-          d = fmaf(t.x, kr[x], d);
-          d = fmaf(t.y, kr[x + 1], d);
-          d = fmaf(t.z, kr[x + 2], d);
-          d = fmaf(t.w, kr[x + 3], d);
+          d0 = fmaf(t.x, kr[x], d0);
+          d1 = fmaf(t.y, kr[x + 1], d1);
+          d0 = fmaf(t.z, kr[x + 2], d0);
+          d1 = fmaf(t.w, kr[x + 3], d1);
         }
-        s[i] = d;
+        s[i] += d0 + d1;
       }
     }
     // Online softmax per item.
@@ -220,10 +221,13 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < AI; i++) {
         if (!live[i]) continue;
-        float o = acc[i][sl];
+        float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-        for (int j = 0; j < AKC; j++) o = fmaf(lane_f(p[i], j), vr[j], o);
-        acc[i][sl] = o;
+        for (int j = 0; j < AKC; j += 2) {
+          o0 = fmaf(lane_f(p[i], j), vr[j], o0);
+          o1 = fmaf(lane_f(p[i], j + 1), vr[j + 1], o1);
+        }
+        acc[i][sl] += o0 + o1;
       }
     }
   }
@@ -280,7 +284,12 @@ int launch_sdpa(AttnArgs a, hipStream_t s) {
   if (G > AW * AI)
     return moe_fail(MOE_INVALID_ARGUMENT, "sdpa: more than " + std::to_string(AW * AI) +
                                               " query heads per kv head");
-  a.rows_per_block = (AW * AI) / G;
+  // Rows per block: up to the 64 items a block holds, fewer for short
+  // sequences so that the grid still has ~512 blocks (each block stages its
+  // keys once; more rows per block share more of them).
+  const int max_rows = (AW * AI) / G;
+  const long want = ((long)a.q_len * a.kv_heads + 511) / 512;
+  a.rows_per_block = (int)std::max(1L, std::min((long)max_rows, want));
   const int ns = a.head_dim <= 64 ? 1 : 2;
   const size_t lds = (size_t)(AW * AI * 64 * ns + 2 * AKC * (64 * ns + 4)) * 4;
   dim3 grid((a.q_len + a.rows_per_block - 1) / a.rows_per_block, a.kv_heads), block(AW * WAVE);

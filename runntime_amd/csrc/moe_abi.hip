@@ -737,6 +737,18 @@ extern "C" int moe_rmsnorm(moe_ctx *ctx, const void *x, moe_dtype dtype, int row
   return after_launch("rmsNorm");
 }
 
+extern "C" int moe_linear(moe_ctx *ctx, const float *x, const float *w, const float *bias,
+                          const float *addend, int T, int K, int N, float *out) {
+  int rc = check_ctx(ctx, "linear");
+  if (rc) return rc;
+  REQUIRE(T >= 1 && K >= 1 && N >= 1, "linear: T, K and N must be positive");
+  REQUIRE(x && w && out, "linear: NULL tensor");
+  if ((rc = moe_ws_ensure(ctx, linear_ws_bytes(T, K, N)))) return rc;
+  if ((rc = launch_linear(x, w, bias, addend, out, (float *)ctx->ws, T, K, N, ctx->stream)))
+    return rc;
+  return after_launch("linear");
+}
+
 extern "C" int moe_rope(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
                         int head_dim, int src_start, int width, const float *cos_t,
                         const float *sin_t, void *out) {

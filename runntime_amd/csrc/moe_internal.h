@@ -237,6 +237,12 @@ struct AttnArgs {
 int launch_rope(const void *x, moe_dtype dt, int rows, int cols, int hd, int src_start, int width,
                 const float *cs, const float *sn, void *out, hipStream_t s);
 int launch_sdpa(AttnArgs a, hipStream_t s);
+// Dense f32 Linear (linear.hip): y = x·W + bias + addend; `part` holds
+// linear_ws_bytes(T, K, N) of K-slice partial products.
+size_t linear_ws_bytes(int T, int K, int N);
+int launch_linear(const float *x, const float *w, const float *bias, const float *addend, float *y,
+                  float *part, int T, int K, int N, hipStream_t s);
+int moe_ws_ensure(moe_ctx *ctx, size_t bytes);
 
 // Float-weight expert products (float.hip): rows grouped by the dispatch,
 // weights row-major [E·K, N] of f32 or f16, biases [E, N] of the same type

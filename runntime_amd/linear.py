@@ -2,15 +2,17 @@
 
 Reference: src/core/nn/layers.ts:166-263 (Linear: y = x·W + bias + addend,
 W stored [in, out], torch checkpoints transposed once at load; a quantized
-checkpoint weight loads as quantW words [in, out] with f32 scales
-[in / groupSize, out]), src/core/graph/compose.ts:45-53 (linear).
+checkpoint weight loads as ints with scales [in / groupSize, out] and its
+kernel multiplies each int by its group's scale), src/core/graph/
+compose.ts:45-53 (linear).
 
-A quantized Linear is the grouped down product with one expert: quantW
-[in, out], scales [in / g, out], bias [1, out], every row routed to expert
-0 with gate 1.0 (exact), the addend as the residual (moe_down). A float
-Linear is matmulGather with one expert (moe_matmul_gather) and takes no
-addend.
+Both kinds run on moe_linear (linear.hip): the weight is kept as f32 [in,
+out], a quantized one dequantized once at load (int · its group's scale,
+one f32 product per weight). The projections of this model are small (a
+few MB per block), and the texts are tens of rows, so the kernel spreads
+the work over columns and K slices rather than streaming int8.
 """
+import ctypes
 from dataclasses import dataclass
 from typing import Optional
 
@@ -18,39 +20,29 @@ import numpy as np
 import torch
 
 from .errors import RunntimeError
-from .quantw import QuantExpertWeight, QuantW, pack_expert_weights
-
-
-def _route_ones(t: int, device) -> torch.Tensor:
-    """[T, 2] route rows (expert 0, gate 1.0) for one-expert calls."""
-    r = torch.empty((t, 2), dtype=torch.float32, device=device)
-    r[:, 0] = 0.0
-    r[:, 1] = 1.0
-    return r
 
 
 @dataclass
 class Linear:
-    """in_features → out_features. Exactly one of `quant` (QuantExpertWeight
-    with E = 1, plus bits and group_size) or `weight` (float [in, out] with
-    `bias` [1, out]) is set."""
+    """in_features → out_features: `weight` f32 [in, out], `bias` f32
+    [out] or None. `bits` / `group_size` record a quantized checkpoint's
+    format (0 for a float one)."""
     in_features: int
     out_features: int
-    quant: Optional[QuantExpertWeight] = None
-    bits: int = 8
-    group_size: int = 0
-    weight: Optional[torch.Tensor] = None
+    weight: torch.Tensor
     bias: Optional[torch.Tensor] = None
+    bits: int = 0
+    group_size: int = 0
 
     @staticmethod
     def from_torch_layout(w_out_in: np.ndarray, bias: Optional[np.ndarray], device) -> "Linear":
         """A float checkpoint weight [out, in] (transposed once, as the
         reference's transformStateDict does)."""
         out_f, in_f = w_out_in.shape
-        w = torch.from_numpy(np.ascontiguousarray(np.asarray(w_out_in).T)).to(device)
-        b = (torch.from_numpy(np.asarray(bias, np.float32).reshape(1, out_f)).to(device).to(w.dtype)
-             if bias is not None else torch.zeros((1, out_f), dtype=w.dtype, device=device))
-        return Linear(in_f, out_f, weight=w, bias=b)
+        w = torch.from_numpy(np.ascontiguousarray(np.asarray(w_out_in, np.float32).T)).to(device)
+        b = (torch.from_numpy(np.asarray(bias, np.float32).reshape(out_f)).to(device)
+             if bias is not None else None)
+        return Linear(in_f, out_f, w, b)
 
     @staticmethod
     def from_quant(ints_out_in: np.ndarray, scales_out_groups: np.ndarray, bits: int,
@@ -60,32 +52,34 @@ class Linear:
         out_f, in_f = ints_out_in.shape
         groups = scales_out_groups.shape[1]
         g = in_f // groups if groups else 0
-        if (groups == 0 or in_f % groups or in_f % 4 or g % 4 or out_f % (32 // bits)):
+        if groups == 0 or in_f % groups:
             raise RunntimeError(
                 "CHECKPOINT_MISMATCH",
-                f"Linear: {name} is int{bits} in groups of {g}, which needs in features a "
-                f"multiple of 4 and of the group size, out features a multiple of {32 // bits} "
-                f"and a group size a multiple of 4, got [out, in] = [{out_f}, {in_f}]")
-        words = pack_expert_weights(np.asarray(ints_out_in, np.int8).T.reshape(1, in_f, out_f),
-                                    bits)
-        sc = np.ascontiguousarray(np.asarray(scales_out_groups, np.float32).T)  # [in/g, out]
-        b = (np.asarray(bias, np.float32).reshape(1, out_f) if bias is not None
-             else np.zeros((1, out_f), np.float32))
-        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
-        q = QuantExpertWeight(QuantW(dev(words.view(np.int32)), (in_f, out_f)), dev(sc), dev(b))
-        return Linear(in_f, out_f, quant=q, bits=bits, group_size=g)
+                f"Linear: {name} is int{bits} with {groups} scale groups, which must divide its "
+                f"{in_f} in features")
+        sc = np.asarray(scales_out_groups, np.float32)
+        w = (np.asarray(ints_out_in, np.float32).reshape(out_f, groups, g) * sc[:, :, None])
+        lin = Linear.from_torch_layout(w.reshape(out_f, in_f), bias, device)
+        lin.bits, lin.group_size = bits, g
+        return lin
 
     def forward(self, x: torch.Tensor, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """y = x·W + bias (+ addend): [T, in] → [T, out]."""
-        from .core import matmulGather, moeDown
+        """y = x·W + bias (+ addend): f32 [T, in] → f32 [T, out]."""
+        from . import _lib
+        from .core import _ctx, _device_of
+        if x.dim() != 2 or x.shape[1] != self.in_features or x.dtype != torch.float32:
+            raise ValueError(f"Linear: x must be f32 [T, {self.in_features}], got "
+                             f"{x.dtype} {list(x.shape)}")
         t = x.shape[0]
-        if x.dim() != 2 or x.shape[1] != self.in_features:
-            raise ValueError(f"Linear: x must be [T, {self.in_features}], got {list(x.shape)}")
-        if self.quant is not None:
-            route = _route_ones(t, x.device)
-            return moeDown(x, route, self.quant, addend,
-                           {"bits": self.bits, "groupSize": self.group_size})
-        if addend is not None:
-            raise ValueError("Linear: a float weight takes no addend here")
-        idx = torch.zeros(t, dtype=torch.float32, device=x.device)
-        return matmulGather(x, self.weight, idx, {"bias": self.bias})
+        if addend is not None and (addend.dtype != torch.float32
+                                   or tuple(addend.shape) != (t, self.out_features)):
+            raise ValueError(f"Linear: addend must be f32 [{t}, {self.out_features}]")
+        x = x.contiguous()
+        dev = _device_of(x, self.weight, *(a for a in (self.bias, addend) if a is not None))
+        out = torch.empty((t, self.out_features), dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        _lib.check(lib.moe_linear(_ctx(dev), x.data_ptr(), self.weight.data_ptr(),
+                                  self.bias.data_ptr() if self.bias is not None else None,
+                                  addend.data_ptr() if addend is not None else None, t,
+                                  self.in_features, self.out_features, out.data_ptr()))
+        return out

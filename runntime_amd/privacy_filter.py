@@ -122,6 +122,60 @@ class PrivacyFilterModel:
         return self.unembed.forward(rmsNorm(x, self.norm_w, RMS_EPS))
 
 
+class GraphedForward:
+    """The model's forward for a set of text lengths captured as HIP graphs
+    (one per length), so a text costs one graph launch instead of ~170
+    launches from Python. Each length keeps its own static input (the
+    embedding rows are copied in before a replay), rope tables and output.
+
+    The library's context workspace grows by reallocation. A graph holds
+    the workspace address it was captured with, so every capture follows an
+    eager forward at the longest length (the workspace each op plans grows
+    with the rows, so the longest length's covers all). Calls of other work
+    on the same device that need a larger workspace would reallocate it
+    under the graphs: run them before building this, or on another
+    device."""
+
+    def __init__(self, model: "PrivacyFilterModel", lengths):
+        self.model = model
+        dev = model.norm_w.device
+        self.stream = torch.cuda.Stream(device=dev)
+        self.graphs = {}
+        lengths = sorted(set(int(t) for t in lengths), reverse=True)
+        cur = torch.cuda.current_stream(dev)
+        self.stream.wait_stream(cur)
+        with torch.cuda.stream(self.stream):
+            for t in lengths[:1]:
+                self._body(*self._statics(t, dev))  # grows the workspace once, longest first
+        for t in lengths:
+            x_in, cos, sin = self._statics(t, dev)
+            with torch.cuda.stream(self.stream):
+                self._body(x_in, cos, sin)          # warm at this length on the capture stream
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                out = self._body(x_in, cos, sin)
+            self.graphs[t] = (g, x_in, out, cos, sin)
+        cur.wait_stream(self.stream)
+
+    def _statics(self, t, dev):
+        cos, sin = rope_constants(t)
+        return (torch.zeros((t, HIDDEN), dtype=torch.float32, device=dev),
+                torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev))
+
+    def _body(self, x, cos, sin):
+        from .core import rmsNorm
+        for b in self.model.blocks:
+            x = b.forward(x, cos, sin)
+        return self.model.unembed.forward(rmsNorm(x, self.model.norm_w, RMS_EPS))
+
+    def __call__(self, token_ids) -> torch.Tensor:
+        ids = np.asarray(token_ids, np.int64)
+        g, x_in, out, _, _ = self.graphs[ids.size]
+        x_in.copy_(torch.from_numpy(np.ascontiguousarray(self.model.embedding[ids], np.float32)))
+        g.replay()
+        return out
+
+
 # ------------------------------------------------------------ decoding (host)
 
 V2_SPAN_CLASS_NAMES = ["O", "account_number", "private_address", "private_date", "private_email",

@@ -108,3 +108,44 @@ def test_model_forward_is_its_block_chain_and_decodes():
     labels = pf.ViterbiDecoder(info).decode(pf.log_softmax_rows(logits[:, :33].cpu().numpy()))
     assert len(labels) == 90 and all(0 <= l < 33 for l in labels)
     assert np.isfinite(hn).all()
+
+
+def test_graphed_forward_replays_equal_eager():
+    # Replays with eager work and synchronisations between them, each against
+    # the eager forward of the same ids (graph nodes must hold no memsets).
+    rng = np.random.default_rng(21)
+    blocks = [pf.Block(make_attn(rng)[0], moe_block(rng)) for _ in range(2)]
+    unembed, _, _ = qlinear(rng, 36, 640, 640, bias=False)
+    emb = rng.standard_normal((50, 640)).astype(np.float32)
+    model = pf.PrivacyFilterModel(emb, blocks, torch.ones(640, device=DEV), unembed)
+    say("graphed forward, lengths 17, 40, 64")
+    gf = pf.GraphedForward(model, [17, 40, 64])
+    for rep in range(3):
+        for t in (40, 17, 64):
+            ids = rng.integers(0, 50, size=t)
+            got = gf(ids).clone()
+            torch.cuda.synchronize()
+            want = model.forward(ids)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), (rep, t)
+
+
+@pytest.mark.parametrize("T,K,N,bias,add", [(1, 640, 1152, True, False), (56, 896, 640, True, True),
+                                            (300, 640, 36, False, False), (1031, 37, 8, True, True),
+                                            (5, 100, 260, False, True)])
+def test_linear_shapes(T, K, N, bias, add):
+    say(f"linear T={T} K={K} N={N} bias={bias} addend={add}")
+    rng = np.random.default_rng(T + K)
+    w = rng.standard_normal((N, K)).astype(np.float32) / np.sqrt(K)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    lin = Linear.from_torch_layout(w, b, DEV)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    a = rng.standard_normal((T, N)).astype(np.float32) if add else None
+    got = lin.forward(torch.from_numpy(x).to(DEV), torch.from_numpy(a).to(DEV) if add else None)
+    torch.cuda.synchronize()
+    want = x.astype(np.float64) @ w.T.astype(np.float64)
+    if bias:
+        want += b
+    if add:
+        want += a
+    np.testing.assert_allclose(got.cpu().numpy(), want, atol=2e-5, rtol=1e-5)
