@@ -25,6 +25,8 @@
  *                                                  src/core/graph/ops/matmul.ts:180-210,
  *                                                  kernel src/core/kernels/matmul/matmulGather.ts
  *   moe_block_float  EagerMoeMlp.forward, float weights  src/zoo/privacy-filter/moeMlp.ts:79-100
+ *   moe_viterbi_decode  ViterbiDecoder.decode (host code, no GPU)
+ *                                                  src/zoo/privacy-filter/viterbi.ts:85-148
  *   moe_linear       Linear.forward(x, {addend}) with a float (or load-time dequantized)
  *                    weight [in, out]             src/core/nn/layers.ts:166-263,
  *                                                  src/core/graph/compose.ts:45-53
@@ -211,6 +213,13 @@ MOE_API int moe_block_float(moe_ctx *ctx, const void *x, moe_dtype dtype, const 
                             const void *glu_w, const void *glu_b, const void *lin_w,
                             const void *lin_b, const void *out_w, const void *out_b, int T, int d,
                             int I, int E, int k, float *route_out, float *out);
+/* The privacy filter's constrained Viterbi decode (src/zoo/privacy-filter/
+ * viterbi.ts:85-148), host memory, no GPU: path [T] = the best label path
+ * under start [n], end [n] and trans [n·n] (prev-major) f64 scores and
+ * log_probs [T, n] f32; ties keep the lower previous / last label; when no
+ * score stays finite, the per-token argmax. */
+MOE_API int moe_viterbi_decode(const double *start, const double *end, const double *trans,
+                               const float *log_probs, int T, int n, int32_t *path);
 /* Linear (src/core/nn/layers.ts:166-263): out [T, N] = x [T, K] · w [K, N]
  * + bias [N] (or NULL) + addend [T, N] (or NULL), all f32, w row-major
  * [in, out] (a quantized checkpoint weight dequantized once at load). Uses

@@ -30,9 +30,18 @@ PER_FILE = {
 SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "pack.hip", "norm.hip", "float.hip", "attn.hip", "linear.hip"]
 
 
+# Host-only C++ (no device code), compiled by the host compiler.
+HOST_SOURCES = ["viterbi.cpp"]
+CXX = os.environ.get("CXX", "g++")
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON, *PER_FILE.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    if src in HOST_SOURCES:
+        cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-c",
+               os.path.join(CSRC, src), "-o", obj]
+    else:
+        cmd = [HIPCC, *COMMON, *PER_FILE.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -42,7 +51,7 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(_compile, SOURCES + HOST_SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

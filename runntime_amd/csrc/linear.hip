@@ -11,7 +11,8 @@
 // rows), so the work is spread over columns and K: block (column tile of
 // 256, K slice of LKS) stages its rows' K slice in LDS and writes a
 // partial product; a second kernel adds the slices in slice order, then the
-// bias and the addend. Each thread owns one column and LRB rows at a time.
+// bias and the addend. Each thread owns one column, its K slice held in
+// registers.
 #include "moe_internal.h"
 
 namespace {
@@ -30,6 +31,12 @@ __global__ __launch_bounds__(LCOLS) void k_linear_partial(const float *__restric
   const int k0 = s * LKS, kl = min(LKS, K - k0);
   const bool col = n < N;
   float *out = part + (int64_t)s * T * N;
+  // The column's K slice in registers, every load issued at once: the row
+  // passes then read only LDS.
+  float wr[LKS];
+#pragma unroll
+  for (int kk = 0; kk < LKS; kk++)
+    wr[kk] = (col && kk < kl) ? w[(int64_t)(k0 + kk) * N + n] : 0.f;
   for (int r0 = 0; r0 < T; r0 += LRB) {
     const int rows = min(LRB, T - r0);
     __syncthreads();
@@ -38,32 +45,20 @@ __global__ __launch_bounds__(LCOLS) void k_linear_partial(const float *__restric
       xs[r][kk] = (r < rows && kk < kl) ? x[(int64_t)(r0 + r) * K + k0 + kk] : 0.f;
     }
     __syncthreads();
-    float acc[LRB];
+    if (!col) continue;
+    // One row at a time over the unrolled slice (register indices stay
+    // static), two chains per row.
+    for (int r = 0; r < rows; r++) {
+      float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int r = 0; r < LRB; r++) acc[r] = 0.f;
-    if (col) {
-      const float *wp = w + (int64_t)k0 * N + n;
-      int kk = 0;
-      for (; kk + 4 <= kl; kk += 4) {
-        const float w0 = wp[(int64_t)kk * N], w1 = wp[(int64_t)(kk + 1) * N];
-        const float w2 = wp[(int64_t)(kk + 2) * N], w3 = wp[(int64_t)(kk + 3) * N];
-#pragma unroll
-        for (int r = 0; r < LRB; r++) {
-          const float4 xv = *(const float4 *)&xs[r][kk];
-          acc[r] = fmaf(xv.x, w0, acc[r]);
-          acc[r] = fmaf(xv.y, w1, acc[r]);
-          acc[r] = fmaf(xv.z, w2, acc[r]);
-          acc[r] = fmaf(xv.w, w3, acc[r]);
-        }
+      for (int kk = 0; kk < LKS; kk += 4) {
+        const float4 xv = *(const float4 *)&xs[r][kk];
+        a0 = fmaf(xv.x, wr[kk], a0);
+        a1 = fmaf(xv.y, wr[kk + 1], a1);
+        a0 = fmaf(xv.z, wr[kk + 2], a0);
+        a1 = fmaf(xv.w, wr[kk + 3], a1);
       }
-      for (; kk < kl; kk++) {
-        const float wv = wp[(int64_t)kk * N];
-#pragma unroll
-        for (int r = 0; r < LRB; r++) acc[r] = fmaf(xs[r][kk], wv, acc[r]);
-      }
-#pragma unroll
-      for (int r = 0; r < LRB; r++)
-        if (r < rows) out[(int64_t)(r0 + r) * N + n] = acc[r];
+      out[(int64_t)(r0 + r) * N + n] = a0 + a1;
     }
   }
 }

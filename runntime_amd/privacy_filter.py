@@ -275,9 +275,9 @@ class ViterbiDecoder:
             return 0.0
 
         bg = info.background_token_label
-        self.start = np.full(n, self.NEG_INF)
-        self.end = np.full(n, self.NEG_INF)
-        self.trans = np.full((n, n), self.NEG_INF)
+        self.start = np.full(n, self.NEG_INF, dtype=np.float64)
+        self.end = np.full(n, self.NEG_INF, dtype=np.float64)
+        self.trans = np.full((n, n), self.NEG_INF, dtype=np.float64)
         for i in range(n):
             t = tag(i)
             if t in ("B", "S") or i == bg:
@@ -289,6 +289,21 @@ class ViterbiDecoder:
                     self.trans[i, j] = bias(i, j)
 
     def decode(self, log_probs: np.ndarray) -> List[int]:
+        """The library's native decode (moe_viterbi_decode)."""
+        import ctypes
+        from . import _lib
+        lp = np.ascontiguousarray(log_probs, np.float32)
+        if lp.ndim != 2 or lp.shape[1] != self.n:
+            raise ValueError(f"Expected width {self.n}, got {lp.shape[-1]}")
+        path = np.zeros(lp.shape[0], np.int32)
+        p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        _lib.check(_lib.load().moe_viterbi_decode(p(self.start), p(self.end), p(self.trans), p(lp),
+                                                  lp.shape[0], self.n, p(path)))
+        return path.tolist()
+
+    def decode_py(self, log_probs: np.ndarray) -> List[int]:
+        """The same decode in numpy (a restatement the native one is tested
+        against)."""
         lp = np.asarray(log_probs, np.float32)
         if lp.ndim != 2 or lp.shape[1] != self.n:
             raise ValueError(f"Expected width {self.n}, got {lp.shape[-1]}")

@@ -40,7 +40,8 @@ def test_viterbi_is_the_best_valid_path(biases, seed):
     dec = pf.ViterbiDecoder(info, biases)
     rng = np.random.default_rng(seed)
     lp = pf.log_softmax_rows(rng.standard_normal((3, 33)).astype(np.float32) * 3)
-    assert dec.decode(lp) == _brute(dec, lp.astype(np.float64))
+    want = _brute(dec, lp.astype(np.float64))
+    assert dec.decode(lp) == want and dec.decode_py(lp) == want
 
 
 def test_viterbi_transitions_follow_bioes():
@@ -81,3 +82,21 @@ def test_log_softmax_rows():
     x = np.random.default_rng(0).standard_normal((4, 33)).astype(np.float32)
     lp = pf.log_softmax_rows(x)
     np.testing.assert_allclose(np.exp(lp.astype(np.float64)).sum(1), 1, rtol=1e-6)
+
+
+@pytest.mark.parametrize("T", [0, 1, 2, 57, 300])
+def test_native_viterbi_equals_the_numpy_one(T):
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info, pf.ViterbiBiases(0.1, -0.3, 0.2, 0.0, -0.1, 0.4))
+    lp = pf.log_softmax_rows(np.random.default_rng(T).standard_normal((T, 33)).astype(np.float32) * 4
+                             ) if T else np.zeros((0, 33), np.float32)
+    assert dec.decode(lp) == dec.decode_py(lp)
+
+
+def test_native_viterbi_falls_back_to_argmax():
+    # every transition forbidden: no finite path, per-token argmax
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info)
+    dec.trans[:] = -np.inf
+    lp = pf.log_softmax_rows(np.random.default_rng(9).standard_normal((6, 33)).astype(np.float32))
+    assert dec.decode(lp) == dec.decode_py(lp) == [int(j) for j in np.argmax(lp, 1)]
