@@ -376,6 +376,128 @@ def labels_to_spans(labels, info: LabelInfo) -> List[TokenSpan]:
 
 # ------------------------------------------------------------------ loading
 
+def transform_hf_state_dict(t: dict) -> dict:
+    """transformHfPrivacyFilterStateDict (stateDictHooks.ts:41-78): maps the
+    official transformers-layout checkpoint ({name: ndarray}) onto this
+    model's names. q|k|v projections stack into one qkv weight and bias
+    (rows in that order); each expert tensor splits by column into glu and
+    lin halves with the expert axis folded into rows ([E, K, 2H] → two
+    [E·K, H]; a [E, 2H] bias → two [E, H]); down_proj folds [E, H, K] →
+    [E·H, K]; the rest renames; score.bias (all zero) is dropped. Returns a
+    new dict; raises CHECKPOINT_MISMATCH for a missing tensor."""
+    from .errors import RunntimeError
+    src = dict(t)
+    out = {}
+
+    def take(name):
+        if name not in src:
+            raise RunntimeError("CHECKPOINT_MISMATCH",
+                                f"privacy-filter state dict: missing tensor '{name}'")
+        return src.pop(name)
+
+    def halves(a):
+        h = a.shape[-1] // 2
+        g, l = a[..., :h], a[..., h:]
+        return (np.ascontiguousarray(g.reshape(-1, h)), np.ascontiguousarray(l.reshape(-1, h)))
+
+    n = 0
+    while f"model.layers.{n}.input_layernorm.weight" in src:
+        hf, d = f"model.layers.{n}", f"block.{n}"
+        out[f"{d}.attn.norm.weight"] = take(f"{hf}.input_layernorm.weight")
+        out[f"{d}.mlp.norm.weight"] = take(f"{hf}.post_attention_layernorm.weight")
+        for suf in ("weight", "bias"):
+            out[f"{d}.attn.qkv.{suf}"] = np.concatenate(
+                [take(f"{hf}.self_attn.{p_}_proj.{suf}") for p_ in ("q", "k", "v")], axis=0)
+            out[f"{d}.attn.out.{suf}"] = take(f"{hf}.self_attn.o_proj.{suf}")
+            out[f"{d}.mlp.gate.{suf}"] = take(f"{hf}.mlp.router.{suf}")
+        out[f"{d}.attn.sinks"] = take(f"{hf}.self_attn.sinks")
+        out[f"{d}.mlp.gluWeight"], out[f"{d}.mlp.linWeight"] = halves(
+            take(f"{hf}.mlp.experts.gate_up_proj"))
+        out[f"{d}.mlp.gluBias"], out[f"{d}.mlp.linBias"] = halves(
+            take(f"{hf}.mlp.experts.gate_up_proj_bias"))
+        dp = take(f"{hf}.mlp.experts.down_proj")
+        out[f"{d}.mlp.outWeight"] = dp.reshape(-1, dp.shape[-1])
+        out[f"{d}.mlp.outBias"] = take(f"{hf}.mlp.experts.down_proj_bias")
+        n += 1
+    out["embedding.weight"] = take("model.embed_tokens.weight")
+    out["norm.weight"] = take("model.norm.weight")
+    out["unembedding.weight"] = take("score.weight")
+    src.pop("score.bias", None)
+    out.update(src)  # anything else passes through under its own name
+    return out
+
+
+@dataclass
+class MoeBlockFloat:
+    """EagerMoeMlp with float weights (moeMlp.ts:85-100) on moe_block_float:
+    glu/lin [E·d, I], out [E·I, d] row-major, biases [E, I] / [E, d]; f32
+    here (an f16 or bf16 checkpoint is widened at load, as the network's
+    activations are f32)."""
+    norm_w: torch.Tensor
+    router_w: torch.Tensor      # f32 [d, E]
+    router_b: Optional[torch.Tensor]
+    glu_w: torch.Tensor
+    glu_b: torch.Tensor
+    lin_w: torch.Tensor
+    lin_b: torch.Tensor
+    out_w: torch.Tensor
+    out_b: torch.Tensor
+    k: int = 4
+    eps: float = RMS_EPS
+
+    def forward(self, x):
+        from .core import moe_block_float
+        return moe_block_float(x, self.norm_w, self.eps, self.router_w, self.router_b, self.glu_w,
+                               self.glu_b, self.lin_w, self.lin_b, self.out_w, self.out_b, k=self.k)
+
+
+def model_from_float_state_dict(sd: dict, device="cuda", k: int = 4) -> "PrivacyFilterModel":
+    """The network from float tensors under this model's names (the output
+    of transform_hf_state_dict): float Linears, float MoE blocks."""
+    from .errors import RunntimeError
+    f32 = lambda a: np.ascontiguousarray(np.asarray(a, np.float32))
+    dev = lambda a: torch.from_numpy(f32(a)).to(device)
+
+    def need(name):
+        if name not in sd:
+            raise RunntimeError("CHECKPOINT_MISMATCH",
+                                f"privacy-filter state dict: missing tensor '{name}'")
+        return sd[name]
+
+    blocks = []
+    n = 0
+    while f"block.{n}.attn.qkv.weight" in sd:
+        p = f"block.{n}"
+        attn = AttnBlock(dev(need(f"{p}.attn.norm.weight")).reshape(-1),
+                         Linear.from_torch_layout(f32(need(f"{p}.attn.qkv.weight")),
+                                                  sd.get(f"{p}.attn.qkv.bias"), device),
+                         Linear.from_torch_layout(f32(need(f"{p}.attn.out.weight")),
+                                                  sd.get(f"{p}.attn.out.bias"), device),
+                         dev(need(f"{p}.attn.sinks")).reshape(-1))
+        gate = f32(need(f"{p}.mlp.gate.weight"))        # torch layout [E, d]
+        gb = sd.get(f"{p}.mlp.gate.bias")
+        mlp = MoeBlockFloat(dev(need(f"{p}.mlp.norm.weight")).reshape(-1), dev(gate.T),
+                            dev(gb) if gb is not None else None,
+                            dev(need(f"{p}.mlp.gluWeight")), dev(need(f"{p}.mlp.gluBias")),
+                            dev(need(f"{p}.mlp.linWeight")), dev(need(f"{p}.mlp.linBias")),
+                            dev(need(f"{p}.mlp.outWeight")), dev(need(f"{p}.mlp.outBias")), k=k)
+        blocks.append(Block(attn, mlp))
+        n += 1
+    emb = f32(need("embedding.weight"))
+    un = f32(need("unembedding.weight"))
+    return PrivacyFilterModel(emb, blocks, dev(need("norm.weight")).reshape(-1),
+                              Linear.from_torch_layout(un, None, device))
+
+
+def load_privacy_filter_hf(path: str, device="cuda", k: int = 4) -> "PrivacyFilterModel":
+    """The official transformers-layout checkpoint (no `model` metadata;
+    detector.ts:40-48 maps it with transformHfPrivacyFilterStateDict)."""
+    from .safetensors import SafetensorsFile
+    f = SafetensorsFile(path)
+    return model_from_float_state_dict(transform_hf_state_dict({n: f.array(n) for n in f.names}),
+                                       device, k)
+
+
 def _linear_from_file(f, name, in_f, out_f, device, bias_name=None):
     """A Linear from its torch-layout checkpoint weight [out, in]: I8/U8 +
     F16 `_scale` (quantized) or float (layers.ts:193-217)."""
