@@ -93,6 +93,9 @@ enum MetaSlot { META_VALID = 0, META_ACTIVE = 1, META_MAXCNT = 2, META_TILES = 3
 
 // Largest token count whose routing and dispatch one block does (fused).
 constexpr int SMALL_T = 16;
+// Calls up to FUSED_T tokens (T·k ≤ FUSED_T·MAX_K) run the router's fold,
+// top-k and dispatch in one block per call.
+constexpr int FUSED_T = 64;
 // Rows per M-tile of the grouped GEMM; the dispatch counts M-tiles with it.
 constexpr int GEMM_TILE_M = 128;
 
@@ -143,7 +146,7 @@ struct RouterArgs {
   float *partial;  // workspace, T·J·E floats per call
   int T, d, E, k, calls;
 };
-// Router + top-k. With T <= SMALL_T and `db` given, the dispatch of each call
+// Router + top-k. With T <= FUSED_T and `db` given, the dispatch of each call
 // is built in the same kernel and `dispatched` is set.
 int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m, bool *dispatched,
                        hipStream_t s);

@@ -227,8 +227,9 @@ __global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
   wave_topk_route<NI>(vals, ra.E, ra.k, lane, ra.route + call * ra.route_cs + (int64_t)t * 2 * ra.k);
 }
 
-// Small calls (T <= 16): one block per call (a wavefront per token, and at
-// least one thread per assignment: 64·max(T, ⌈T·k / 64⌉) threads) does the fold
+// Small calls (T ≤ 64): one block per call (a wavefront per token, up to 16
+// wavefronts that then take several tokens each, and at least one thread per
+// assignment: 64·max(min(T, 16), ⌈T·k / 64⌉) threads) does the fold
 // and top-k of every token, then the call's dispatch (dispatch_dev.h) from
 // the ids it just chose — no second pass over the route. An assignment's
 // place within its expert is its rank among the earlier assignments with
@@ -237,15 +238,15 @@ __global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
 template <int NI, int FB>
 __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs ra, DispatchBufs db,
                                                                     int tile_m) {
-  __shared__ __align__(16) int32_t sid[SMALL_T * MAX_K];
+  __shared__ __align__(16) int32_t sid[FUSED_T * MAX_K];
   __shared__ int32_t hist[DISPATCH_MAX_E];
   __shared__ int32_t cursor[DISPATCH_MAX_E + 1];
   const int lane = threadIdx.x & (moe_dev::WAVE - 1);
-  const int t = threadIdx.x / moe_dev::WAVE;
+  const int nwaves = blockDim.x / moe_dev::WAVE;
   const int call = blockIdx.x;
   const int E = ra.E, k = ra.k, A = ra.T * ra.k;
   for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
-  if (t < ra.T) {
+  for (int t = threadIdx.x / moe_dev::WAVE; t < ra.T; t += nwaves) {
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
     const float *partial = ra.partial + call * ((int64_t)ra.T * J * E);
     const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
@@ -404,7 +405,7 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
   MOE_NONNULL(ra.partial);
   MOE_NONNULL(ra.route);
   if (ra.E > ROUTER_MAX_E) return moe_fail(MOE_INVALID_ARGUMENT, "router: more than 512 experts");
-  const bool fuse = db && ra.T <= SMALL_T;
+  const bool fuse = db && ra.T <= FUSED_T && ra.T * ra.k <= FUSED_T * MAX_K;
   // Many tokens: the register-tiled chunk kernel (64 or 32 experts a block).
   if (!fuse && ra.T > SMALL_T && ra.E >= 32) {
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
@@ -435,8 +436,10 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
   const int fb = ni > 2 || Jc <= 8 ? 8 : Jc <= 16 ? 16 : 32;
   if (dispatched) *dispatched = fuse;
   if (fuse) {
-    const int fused_waves = std::max(ra.T, (ra.T * ra.k + WAVE - 1) / WAVE);
-    const int fused_threads = WAVE * fused_waves;  // ≤ 1024: T ≤ 16, k ≤ 16
+    // A wavefront per token up to 16 (more tokens loop), and at least one
+    // thread per assignment (T·k ≤ 1024).
+    const int fused_waves = std::max(std::min(ra.T, 16), (ra.T * ra.k + WAVE - 1) / WAVE);
+    const int fused_threads = WAVE * fused_waves;  // ≤ 1024
     MOE_NONNULL(db->offsets);
     MOE_NONNULL(db->perm);
     if (db->E != ra.E || db->A != ra.T * ra.k)

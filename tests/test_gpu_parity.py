@@ -338,6 +338,25 @@ def test_moe_layer_configs(cid, sample):
     assert all(len(set(r)) == k for r in ids.tolist())
 
 
+@pytest.mark.parametrize("T,E,k,x_dtype", [(64, 64, 16, "f32"), (17, 32, 8, "f16"),
+                                           (64, 128, 4, "f32"), (65, 16, 4, "f32")])
+def test_moe_layer_fused_router_dispatch_limits(T, E, k, x_dtype):
+    """Calls of up to 64 tokens (T·k ≤ 1024) route and dispatch in one
+    kernel whose wavefronts take several tokens each; 65 tokens take the
+    separate dispatch. Routes bit-exact, outputs at the layer bar."""
+    from runntime_amd.synth import MoeConfig
+    cfg = MoeConfig(f"fused_T{T}_E{E}_k{k}", T, 256, E, k, 256, x_dtype)
+    say(f"moe_layer {cfg.name}")
+    inp = make_inputs(cfg, seed=T + E, keep_q=True, bias_rand=True)
+    out, route = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                              inp.residual, k, return_route=True)
+    got_out, got_route = host(out), host(route)
+    tokens = np.arange(T)
+    want_route, want_out, _ = _oracle_layer(inp, tokens)
+    assert np.array_equal(got_route[:, :k], want_route[:, :k]), "expert ids differ"
+    assert_close(got_out, want_out, what=f"{cfg.name} output")
+
+
 def test_moe_layer_matches_ops():
     """moe_layer = topk(router) → moeUp → moeDown composed from the ops."""
     cfg = CONFIGS[1]
