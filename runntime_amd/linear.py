@@ -12,7 +12,6 @@ one f32 product per weight). The projections of this model are small (a
 few MB per block), and the texts are tens of rows, so the kernel spreads
 the work over columns and K slices rather than streaming int8.
 """
-import ctypes
 from dataclasses import dataclass
 from typing import Optional
 

@@ -18,7 +18,7 @@ grouped down product or matmulGather, rope, sdpa, moe_block); the
 embedding table stays on the host as the reference keeps it on the CPU.
 """
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import List, Optional
 
 import numpy as np

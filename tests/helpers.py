@@ -1,6 +1,5 @@
 """Shared test helpers: the reference tests' input generators and the
 tolerance checks."""
-import math
 
 import numpy as np
 
