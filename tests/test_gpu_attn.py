@@ -188,3 +188,24 @@ def test_rope_past_2p24_elements():
 
 def test_rope_f16_past_2p24_pairs():
     check_rope(2 ** 14 + 1, 2048, 64, dtype="f16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_sdpa_long_sequence_sampled_rows(dtype):
+    """T = 4096 with the privacy filter's window and sinks; rows checked on
+    three ranges, each against the oracle run on those rows as queries at
+    their positions (qPosOffset) over all keys."""
+    T, qh, kvh, hd = 4096, 14, 2, 64
+    say(f"sdpa long {dtype} T={T}")
+    rng = np.random.default_rng(8)
+    q = rnd((rng.standard_normal((T, qh * hd)) * 2 / math.sqrt(hd)).astype(np.float32), dtype)
+    k = rnd(rng.standard_normal((T, kvh * hd)).astype(np.float32), dtype)
+    v = rnd(rng.standard_normal((T, kvh * hd)).astype(np.float32), dtype)
+    sinks = rng.standard_normal(qh).astype(np.float32)
+    t = TD[dtype]
+    got = rt.sdpa(dev(q, t), dev(k, t), dev(v, t),
+                  dict(qHeads=qh, kvHeads=kvh, headDim=hd, windowLeft=128, windowRight=128,
+                       sinks=dev(sinks))).float().cpu().numpy()
+    for r0 in (0, 2000, T - 64):
+        want = ref.sdpa_f64(q[r0:r0 + 64], k, v, qh, kvh, hd, 128, 128, r0, sinks)
+        np.testing.assert_allclose(got[r0:r0 + 64], want, **TOL[dtype])
