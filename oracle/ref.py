@@ -262,3 +262,31 @@ def sdpa_f64(q, k, v, q_heads, kv_heads, head_dim, window_left=np.inf, window_ri
         num = np.einsum("hj,jhx->hx", p, v[:, kh, :])
         out[i] = np.where(ok[:, None], num / np.where(ok, den, 1.0)[:, None], 0.0)
     return out.reshape(q_len, q_heads * head_dim)
+
+
+def viterbi_decode(start, end, trans, log_probs):
+    """ViterbiDecoder.decode (src/zoo/privacy-filter/viterbi.ts:85-148) in
+    numpy: f64 scores over f32 log-probabilities, ties to the lower previous
+    label (the first maximum) and the lower last label; with no finite
+    score left, the per-token argmax."""
+    lp = np.asarray(log_probs, np.float32)
+    T, n = lp.shape
+    if T == 0:
+        return []
+    lp64 = lp.astype(np.float64)
+    scores = lp64[0] + start
+    back = np.zeros((max(T - 1, 0), n), np.int32)
+    for t in range(1, T):
+        cand = scores[:, None] + trans
+        bi = np.argmax(cand, axis=0)
+        back[t - 1] = bi
+        scores = cand[bi, np.arange(n)] + lp64[t]
+    if not np.isfinite(scores).any():
+        return [int(j) for j in np.argmax(lp, axis=1)]
+    last = int(np.argmax(scores + end))
+    path = [0] * T
+    path[T - 1] = last
+    for t in range(T - 2, -1, -1):
+        last = int(back[t, path[t + 1]])
+        path[t] = last
+    return path

@@ -289,7 +289,9 @@ class ViterbiDecoder:
                     self.trans[i, j] = bias(i, j)
 
     def decode(self, log_probs: np.ndarray) -> List[int]:
-        """The library's native decode (moe_viterbi_decode)."""
+        """The library's native decode (moe_viterbi_decode): ties keep the
+        lower previous label and the lower last label; with no finite path,
+        the per-token argmax."""
         import ctypes
         from . import _lib
         lp = np.ascontiguousarray(log_probs, np.float32)
@@ -300,33 +302,6 @@ class ViterbiDecoder:
         _lib.check(_lib.load().moe_viterbi_decode(p(self.start), p(self.end), p(self.trans), p(lp),
                                                   lp.shape[0], self.n, p(path)))
         return path.tolist()
-
-    def decode_py(self, log_probs: np.ndarray) -> List[int]:
-        """The same decode in numpy (a restatement the native one is tested
-        against)."""
-        lp = np.asarray(log_probs, np.float32)
-        if lp.ndim != 2 or lp.shape[1] != self.n:
-            raise ValueError(f"Expected width {self.n}, got {lp.shape[-1]}")
-        T = lp.shape[0]
-        if T == 0:
-            return []
-        lp64 = lp.astype(np.float64)
-        scores = lp64[0] + self.start
-        back = np.zeros((max(T - 1, 0), self.n), np.int32)
-        for t in range(1, T):
-            cand = scores[:, None] + self.trans        # [prev, next]
-            best_i = np.argmax(cand, axis=0)            # first maximum: the lower prev
-            back[t - 1] = best_i
-            scores = cand[best_i, np.arange(self.n)] + lp64[t]
-        if not np.isfinite(scores).any():
-            return [int(j) for j in np.argmax(lp, axis=1)]
-        last = int(np.argmax(scores + self.end))
-        path = [0] * T
-        path[T - 1] = last
-        for t in range(T - 2, -1, -1):
-            last = int(back[t, path[t + 1]])
-            path[t] = last
-        return path
 
 
 @dataclass

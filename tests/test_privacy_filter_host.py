@@ -1,6 +1,7 @@
 """Host-side pieces of the privacy-filter model (runntime_amd/
-privacy_filter.py): the constrained Viterbi decoder against brute force over
-every label path (viterbi.ts:20-148 defines the best-scoring valid path),
+privacy_filter.py): the constrained Viterbi decoder (native, and the
+oracle's numpy restatement) against brute force over every label path
+(viterbi.ts:20-148 defines the best-scoring valid path),
 the label info (config.ts:1-75), token spans (spans.ts:18-70), the YaRN
 rope tables at their closed-form limits (rope.ts:24-94) and log-softmax."""
 import itertools
@@ -9,6 +10,7 @@ import math
 import numpy as np
 import pytest
 
+from oracle import ref
 from runntime_amd import privacy_filter as pf
 
 
@@ -41,7 +43,7 @@ def test_viterbi_is_the_best_valid_path(biases, seed):
     rng = np.random.default_rng(seed)
     lp = pf.log_softmax_rows(rng.standard_normal((3, 33)).astype(np.float32) * 3)
     want = _brute(dec, lp.astype(np.float64))
-    assert dec.decode(lp) == want and dec.decode_py(lp) == want
+    assert dec.decode(lp) == want and ref.viterbi_decode(dec.start, dec.end, dec.trans, lp) == want
 
 
 def test_viterbi_transitions_follow_bioes():
@@ -90,7 +92,7 @@ def test_native_viterbi_equals_the_numpy_one(T):
     dec = pf.ViterbiDecoder(info, pf.ViterbiBiases(0.1, -0.3, 0.2, 0.0, -0.1, 0.4))
     lp = pf.log_softmax_rows(np.random.default_rng(T).standard_normal((T, 33)).astype(np.float32) * 4
                              ) if T else np.zeros((0, 33), np.float32)
-    assert dec.decode(lp) == dec.decode_py(lp)
+    assert dec.decode(lp) == ref.viterbi_decode(dec.start, dec.end, dec.trans, lp)
 
 
 def test_native_viterbi_falls_back_to_argmax():
@@ -99,4 +101,4 @@ def test_native_viterbi_falls_back_to_argmax():
     dec = pf.ViterbiDecoder(info)
     dec.trans[:] = -np.inf
     lp = pf.log_softmax_rows(np.random.default_rng(9).standard_normal((6, 33)).astype(np.float32))
-    assert dec.decode(lp) == dec.decode_py(lp) == [int(j) for j in np.argmax(lp, 1)]
+    assert dec.decode(lp) == ref.viterbi_decode(dec.start, dec.end, dec.trans, lp) == [int(j) for j in np.argmax(lp, 1)]
