@@ -5,7 +5,8 @@
 //   k_dispatch_count   per 1024-assignment tile: LDS histogram
 //   k_dispatch_scan    one block per call: offsets, M-tile offsets, active
 //                      list, per-tile bases; marks unused perm slots −1
-//   k_dispatch_scatter per tile: stable rank via wavefront ballots, then place
+//   k_dispatch_scatter per tile: stable rank via wavefront ballots (one per id
+//                      bit), then place
 #include "dispatch_dev.h"
 
 namespace {

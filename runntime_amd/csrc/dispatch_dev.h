@@ -104,17 +104,17 @@ __device__ __forceinline__ void block_place(int e, int64_t a, int E, int32_t *cu
   __syncthreads();
   int rank = 0;
   if (wave < 4) {
-    // Rank among earlier lanes of this wavefront with the same expert.
-    uint64_t pending = __ballot(e >= 0);
-    while (pending) {
-      int leader = __ffsll((unsigned long long)pending) - 1;
-      int el = __shfl(e, leader);
-      uint64_t same = __ballot(e == el) & pending;
-      if (e == el) {
-        rank = __popcll(same & ((1ull << lane) - 1ull));
-        if (lane == leader) wc[wave * E + el] = __popcll(same);
-      }
-      pending &= ~same;
+    // The lanes of this wavefront with the same expert, from one ballot per
+    // bit of the id (lanes whose bit agrees), then the rank among the
+    // earlier ones; the first such lane records the wavefront's count.
+    uint64_t same = __ballot(e >= 0);
+    for (int bit = 0; (1 << bit) < E; bit++) {
+      const uint64_t ones = __ballot(e >= 0 && ((e >> bit) & 1));
+      same &= ((e >> bit) & 1) ? ones : ~ones;
+    }
+    if (e >= 0) {
+      rank = __popcll(same & ((1ull << lane) - 1ull));
+      if (rank == 0) wc[wave * E + e] = __popcll(same);
     }
   }
   __syncthreads();
