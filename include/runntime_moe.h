@@ -30,6 +30,9 @@
  *   moe_linear       Linear.forward(x, {addend}) with a float (or load-time dequantized)
  *                    weight [in, out]             src/core/nn/layers.ts:166-263,
  *                                                  src/core/graph/compose.ts:45-53
+ *   moe_attention    the privacy filter's attention core, rope(q), rope(k), sdpa over one
+ *                    qkv tensor (src/zoo/privacy-filter/attnBlock.ts:39-55); no single
+ *                    reference op: the three calls fused into one kernel
  *   moe_rope         rope(x, cos, sin, {headDim, srcStart, width})
  *                                                  src/core/graph/ops/attention.ts:220-262,
  *                                                  kernel src/core/kernels/attention/rope.ts
@@ -226,6 +229,17 @@ MOE_API int moe_viterbi_decode(const double *start, const double *end, const dou
  * the context workspace for K-slice partial products. */
 MOE_API int moe_linear(moe_ctx *ctx, const float *x, const float *w, const float *bias,
                        const float *addend, int T, int K, int N, float *out);
+/* The attention core of the privacy filter's block (src/zoo/privacy-filter/
+ * attnBlock.ts:39-55): over one qkv tensor [T, (q_heads + 2·kv_heads)·
+ * head_dim] read in place, q and k are roped with cos/sin (f32 [T,
+ * head_dim], pair-duplicated, scale folded in) as they are staged, then the
+ * banded sdpa of moe_sdpa (q_pos_offset 0, no segments or key bias) writes
+ * out [T, q_heads·head_dim]. It equals moe_rope on the q and k column
+ * blocks followed by moe_sdpa, in one kernel; it has no single counterpart
+ * in the reference. */
+MOE_API int moe_attention(moe_ctx *ctx, const void *qkv, moe_dtype dtype, int T, int q_heads,
+                          int kv_heads, int head_dim, int64_t window_left, int64_t window_right,
+                          const float *sinks, const float *cos_t, const float *sin_t, void *out);
 /* rope (src/core/graph/ops/attention.ts:220-262): out [rows, width] =
  * the interleaved pairs of x's columns [src_start, src_start + width)
  * rotated by cos/sin (f32 [rows, head_dim], pair-duplicated, any scale

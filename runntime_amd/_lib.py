@@ -24,7 +24,7 @@ EXPORTED = (
     "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
     "moe_weights_upload", "moe_weights_view", "moe_weights_dispose", "moe_weights_release",
     "moe_block", "moe_rmsnorm", "moe_matmul_gather", "moe_block_float", "moe_rope",
-    "moe_sdpa", "moe_linear", "moe_viterbi_decode",
+    "moe_sdpa", "moe_linear", "moe_viterbi_decode", "moe_attention",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine", "norm")
 
@@ -92,6 +92,7 @@ def load() -> ctypes.CDLL:
             "moe_rope": ([P, P, I, I, I, I, I, I, P, P, P], I),
             "moe_linear": ([P, P, P, P, P, I, I, I, P], I),
             "moe_viterbi_decode": ([P, P, P, P, I, I, P], I),
+            "moe_attention": ([P, P, I, I, I, I, I, ctypes.c_int64, ctypes.c_int64, P, P, P, P], I),
             "moe_sdpa": ([P, I, P, ctypes.c_int64, P, ctypes.c_int64, P, ctypes.c_int64, I, I, I,
                           I, I, ctypes.c_int64, ctypes.c_int64, I, P, P, I, I, I, ctypes.c_float,
                           P], I),

@@ -35,6 +35,16 @@ __device__ __forceinline__ float ld(const _Float16 *p, int64_t i) { return (floa
 __device__ __forceinline__ void st(float *p, int64_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void st(_Float16 *p, int64_t i, float v) { p[i] = (_Float16)v; }
 
+// Element x of a head row after rope (rope.ts:55-66): pair (x0, x1) =
+// (x & ~1, x | 1), out[2p] = x0·c − x1·s, out[2p+1] = x1·c + x0·s; c and s
+// are the pair-duplicated table entries of the element's row.
+template <typename T>
+__device__ __forceinline__ float roped(const T *p, int64_t i, int x, float c, float s) {
+  const int64_t pair = i - (x & 1);
+  const float x0 = ld(p, pair), x1 = ld(p, pair + 1);
+  return (x & 1) ? x1 * c + x0 * s : x0 * c - x1 * s;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 1; m < WAVE; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
@@ -96,7 +106,10 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
     float val = 0.f;
     if (it < nitems && x < hd) {
       const int r = row0 + it / G, h = kvh * G + it % G;
-      val = ld(q, (int64_t)r * a.q_rs + (int64_t)h * hd + x);
+      const int64_t qi = (int64_t)r * a.q_rs + (int64_t)h * hd + x;
+      val = a.rope_cos ? roped(q, qi, x, a.rope_cos[(int64_t)r * hd + x],
+                               a.rope_sin[(int64_t)r * hd + x])
+                       : ld(q, qi);
     }
     qs[e] = val;
   }
@@ -149,7 +162,10 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
       const int key = c0 + j;
       float kv = 0.f, vv = 0.f;
       if (key <= bhi && x < hd) {
-        kv = ld(k, (int64_t)key * a.k_rs + (int64_t)kvh * hd + x);
+        const int64_t ki = (int64_t)key * a.k_rs + (int64_t)kvh * hd + x;
+        kv = a.rope_cos ? roped(k, ki, x, a.rope_cos[(int64_t)key * hd + x],
+                                a.rope_sin[(int64_t)key * hd + x])
+                        : ld(k, ki);
         vv = ld(v, (int64_t)key * a.v_rs + (int64_t)kvh * hd + x);
       }
       ks[j * KST + x] = kv;

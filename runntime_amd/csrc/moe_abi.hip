@@ -749,6 +749,42 @@ extern "C" int moe_linear(moe_ctx *ctx, const float *x, const float *w, const fl
   return after_launch("linear");
 }
 
+extern "C" int moe_attention(moe_ctx *ctx, const void *qkv, moe_dtype dtype, int T, int q_heads,
+                             int kv_heads, int head_dim, int64_t window_left,
+                             int64_t window_right, const float *sinks, const float *cos_t,
+                             const float *sin_t, void *out) {
+  int rc = check_ctx(ctx, "attention");
+  if (rc) return rc;
+  REQUIRE(dtype == MOE_F32 || dtype == MOE_F16, "attention: dtype must be f32 or f16");
+  REQUIRE(T >= 1, "attention: T must be positive");
+  REQUIRE(kv_heads > 0 && q_heads > 0 && q_heads % kv_heads == 0,
+          "attention: qHeads " + S(q_heads) + " not divisible by kvHeads " + S(kv_heads));
+  REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 128,
+          "attention: headDim " + S(head_dim) + " must be even and at most 128");
+  REQUIRE(qkv && cos_t && sin_t && out, "attention: NULL tensor");
+  const int64_t width = (int64_t)(q_heads + 2 * kv_heads) * head_dim;
+  const size_t es = dtype == MOE_F16 ? 2 : 4;
+  AttnArgs a{};
+  a.q = qkv;
+  a.k = (const char *)qkv + (size_t)q_heads * head_dim * es;
+  a.v = (const char *)qkv + (size_t)(q_heads + kv_heads) * head_dim * es;
+  a.q_rs = a.k_rs = a.v_rs = width;
+  a.out = out;
+  a.o_rs = (int64_t)q_heads * head_dim;
+  a.dtype = dtype;
+  a.q_len = a.kv_len = T;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.window_left = window_left < 0 ? -1 : window_left;
+  a.window_right = window_right < 0 ? -1 : window_right;
+  a.sinks = sinks;
+  a.rope_cos = cos_t;
+  a.rope_sin = sin_t;
+  if ((rc = launch_sdpa(a, ctx->stream))) return rc;
+  return after_launch("attention");
+}
+
 extern "C" int moe_rope(moe_ctx *ctx, const void *x, moe_dtype dtype, int rows, int cols,
                         int head_dim, int src_start, int width, const float *cos_t,
                         const float *sin_t, void *out) {

@@ -235,6 +235,9 @@ struct AttnArgs {
   const float *segs;
   int has_kb, kb_start, kb_end;
   float kb_value;
+  // Optional rope of q and k while staging (f32 [rows, head_dim] tables,
+  // pair-duplicated, indexed by the q / k row), or NULL.
+  const float *rope_cos, *rope_sin;
   int rows_per_block;  // set by the launcher
 };
 int launch_rope(const void *x, moe_dtype dt, int rows, int cols, int hd, int src_start, int width,

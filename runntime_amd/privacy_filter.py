@@ -78,15 +78,15 @@ class AttnBlock:
     sinks: torch.Tensor    # f32 [14]
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        from .core import _sdpa_launch, rmsNorm, rope
+        from . import _lib
+        from .core import _ctx, _xdtype, rmsNorm
         t = x.shape[0]
         qkv = self.qkv.forward(rmsNorm(x, self.norm_w, RMS_EPS))            # [T, 1152] f32
-        q = rope(qkv, cos, sin, {"headDim": HEAD, "srcStart": 0, "width": K_OFF})
-        k = rope(qkv, cos, sin, {"headDim": HEAD, "srcStart": K_OFF, "width": KV_HEADS * HEAD})
-        es = qkv.element_size()
-        attn = _sdpa_launch(qkv.device, q.data_ptr(), K_OFF, k.data_ptr(), KV_HEADS * HEAD,
-                            qkv.data_ptr() + V_OFF * es, QKV_WIDTH, t, t, Q_HEADS, KV_HEADS, HEAD,
-                            WINDOW, WINDOW, 0, self.sinks, None, None, qkv.dtype)
+        # rope(q), rope(k) and the banded sdpa in one kernel (moe_attention)
+        attn = torch.empty((t, K_OFF), dtype=qkv.dtype, device=qkv.device)
+        _lib.check(_lib.load().moe_attention(
+            _ctx(qkv.device), qkv.data_ptr(), _xdtype(qkv), t, Q_HEADS, KV_HEADS, HEAD, WINDOW,
+            WINDOW, self.sinks.data_ptr(), cos.data_ptr(), sin.data_ptr(), attn.data_ptr()))
         return self.out.forward(attn, addend=x)
 
 

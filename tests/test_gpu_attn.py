@@ -209,3 +209,33 @@ def test_sdpa_long_sequence_sampled_rows(dtype):
     for r0 in (0, 2000, T - 64):
         want = ref.sdpa_f64(q[r0:r0 + 64], k, v, qh, kvh, hd, 128, 128, r0, sinks)
         np.testing.assert_allclose(got[r0:r0 + 64], want, **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("T", [1, 57, 300])
+def test_fused_attention_core(dtype, T):
+    """moe_attention (rope of the q and k blocks, then banded sdpa over one
+    qkv tensor, attnBlock.ts:39-55) against the oracle's rope_f64 and
+    sdpa_f64 composed, at the sdpa tolerance."""
+    from runntime_amd import _lib
+    from runntime_amd.core import _ctx, _xdtype
+    from runntime_amd import privacy_filter as pf
+    qh, kvh, hd = 14, 2, 64
+    say(f"moe_attention {dtype} T={T}")
+    rng = np.random.default_rng(T)
+    qkv = rnd(rng.standard_normal((T, (qh + 2 * kvh) * hd)).astype(np.float32), dtype)
+    sinks = rng.standard_normal(qh).astype(np.float32)
+    cos, sin = pf.rope_constants(T)
+    t = TD[dtype]
+    # every device tensor held until the kernel has run
+    dq, ds, dc, dsn = dev(qkv, t), dev(sinks), dev(cos), dev(sin)
+    out = torch.empty((T, qh * hd), dtype=t, device=DEV)
+    _lib.check(_lib.load().moe_attention(_ctx(dq.device), dq.data_ptr(), _xdtype(dq), T, qh, kvh,
+                                         hd, 128, 128, ds.data_ptr(), dc.data_ptr(),
+                                         dsn.data_ptr(), out.data_ptr()))
+    torch.cuda.synchronize()
+    q = ref.rope_f64(qkv, cos, sin, hd, 0, qh * hd)
+    k = ref.rope_f64(qkv, cos, sin, hd, qh * hd, kvh * hd)
+    v = qkv[:, (qh + kvh) * hd:].astype(np.float64)
+    want = ref.sdpa_f64(q, k, v, qh, kvh, hd, 128, 128, 0, sinks)
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, **TOL[dtype])
