@@ -62,7 +62,8 @@ def layer_flops(cfg):
 # FETCH_SIZE / WRITE_SIZE counter passes (calibrated against a plain copy);
 # valid for the default launch shape of each workload.
 TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md",
-                    3: "k_expert_skinny_up_c3_decode_traffic.md"}
+                    3: "k_expert_skinny_up_c3_batched_decode_traffic.md",
+                    "3-sequential": "k_expert_skinny_up_c3_decode_traffic.md"}
 
 
 def profiled_traffic(config, default_shape):
@@ -134,6 +135,35 @@ def bench_decode(cfg, args):
                 residual[j0:j0 + n], cfg.k, out=out[j0:j0 + n], route=routes[j0:j0 + n])
 
     return step, n_tok
+
+
+def bench_small_batched(cfg, args):
+    """config 3 (default 16 calls; --c3-calls 0 runs them one at a time): N
+    independent T-token calls per step, one moe_layer_batched launch, call c
+    on weight copy c (no weights shared, so every call streams its own
+    active experts' bytes). The same method as config 2's batched calls."""
+    N = args.c3_calls
+    say(f"drawing {N} weight copies of {cfg.name} on the GPU")
+    wc = make_weight_copies(cfg, N, seed=400, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(9)
+    xdt = torch.float16 if cfg.x_dtype == "f16" else torch.float32
+    x = torch.randn((N, cfg.T, cfg.d), generator=g, device="cuda").to(xdt)
+    residual = torch.zeros((N, cfg.T, cfg.d), dtype=torch.float32, device="cuda")
+    out = torch.empty((N, cfg.T, cfg.d), dtype=torch.float32, device="cuda")
+    routes = torch.empty((N, cfg.T, 2 * cfg.k), dtype=torch.float32, device="cuda")
+    perf.reserve_batched(N, cfg.T, cfg.d, cfg.I, cfg.E, cfg.k)
+
+    def step():
+        rt.moe_layer_batched(x, wc.router_w, wc.router_b, wc.glu, wc.lin, wc.down, residual,
+                             cfg.k, out=out, route=routes)
+
+    def active():
+        step()
+        torch.cuda.synchronize()
+        ids = routes[:, :, :cfg.k].long()
+        return sum(int(torch.unique(ids[c]).numel()) for c in range(N)) / N
+
+    return step, N * cfg.T, active
 
 
 def sequential_rate(cfg, args):
@@ -357,6 +387,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--copies", type=int, default=2, help="rotating input sets (config 3)")
+    ap.add_argument("--c3-calls", type=int, default=16,
+                    help="config 3: N independent calls (own weight copies) per batched launch; "
+                         "0 runs --copies calls one at a time")
     ap.add_argument("--calls-per-launch", type=int, default=1000,
                     help="config 2: independent single-token calls per batched launch")
     ap.add_argument("--no-graph", action="store_true")
@@ -397,8 +430,11 @@ def main():
         return
     cfg = CONFIGS[args.config]
 
+    c3_active = None
     if args.config == 2:
         step, tokens_per_step = bench_decode(cfg, args)
+    elif args.config == 3 and args.c3_calls > 0:
+        step, tokens_per_step, c3_active = bench_small_batched(cfg, args)
     else:
         C = args.copies if args.config == 3 else 1
         say(f"building {C} input set(s) of {cfg.name}")
@@ -459,7 +495,12 @@ def main():
         active_per_call = cfg.k
         calls = tokens_per_step
         W = args.calls_per_launch
+    elif c3_active is not None:
+        active_per_call = c3_active()
+        calls = tokens_per_step // cfg.T
+        W = args.c3_calls
     else:
+        W = 1
         counts = []
         for w in sets:
             r = rt.router_topk(w.x, w.router_w, w.router_b, cfg.k)
@@ -469,10 +510,12 @@ def main():
     up_ms, up_n = groups.get("up", (0.0, 0))
     up_avg_s = up_ms / max(up_n, 1) / 1e3
     default_shape = ((args.config == 2 and args.calls_per_launch == 1000)
-                     or (args.config == 3 and args.copies == 2) or args.config in (4, 5))
-    traffic, traffic_src = profiled_traffic(args.config, default_shape)
+                     or (args.config == 3 and args.c3_calls in (0, 16) and args.copies == 2)
+                     or args.config in (4, 5))
+    traffic, traffic_src = profiled_traffic(
+        "3-sequential" if args.config == 3 and args.c3_calls == 0 else args.config, default_shape)
     if args.config in (2, 3):
-        per_launch = round(up_kernel_bytes(cfg, active_per_call) * (W if args.config == 2 else 1))
+        per_launch = round(up_kernel_bytes(cfg, active_per_call) * W)
         achieved = per_launch / up_avg_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -501,9 +544,10 @@ def main():
         "config": {"workload": cfg.name, "T": cfg.T, "d": cfg.d, "E": cfg.E, "k": cfg.k,
                    "I": cfg.I, "x_dtype": cfg.x_dtype, "tokens_per_step": tokens_per_step,
                    "calls_per_step": calls,
-                   "calls_per_launch": args.calls_per_launch if args.config == 2 else 1,
+                   "calls_per_launch": W if args.config in (2, 3) else 1,
                    "weight_copies": (args.calls_per_launch if args.config == 2
-                                     else args.copies if args.config == 3 else 1),
+                                     else (args.c3_calls or args.copies) if args.config == 3
+                                     else 1),
                    "graph": graph is not None, "parallelism": "single GPU",
                    "arith": "int8 weights exact in f16 MFMA, f32 inputs split hi+lo, f32 accumulate"},
         "layer_roofline_frac": round(layer_frac, 4),

@@ -656,9 +656,13 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     const size_t a_bytes = (size_t)q.rc * a_stage_kp(ea.K) * 2 * (split ? 2 : 1);
     int nw = a_bytes <= 8192 ? 1 : a_bytes <= 16384 ? 2 : 4;
     const int ncg = (ea.N / 4 + 15) / 16;
-    // Longer streams (NS = 2) while they still give ≥ 2 wavefronts per SIMD.
+    // Longer streams (NS = 2) for short units (K < 1024: a 4-column unit
+    // under 4 KB) while they still give ≥ 2 wavefronts per SIMD. Units of
+    // 4 KB and more already stream long enough: batched config-3 calls
+    // (K = 2048 and 1408) measured NS = 1 faster at 2-16 calls per launch
+    // (up 64-78% against 54-74% of HBM).
     const long waves_ns2 = (long)ea.calls * max_active * (MODE == MODE_UP ? ncg : (ncg + 1) / 2);
-    int ns = waves_ns2 >= 2048 ? 2 : 1;
+    int ns = (waves_ns2 >= 2048 && ea.K < 1024) ? 2 : 1;
     // Tuning overrides (MOE_SKINNY_NS = 1|2, MOE_SKINNY_NW = 1|2|4).
     static const int env_ns = getenv("MOE_SKINNY_NS") ? atoi(getenv("MOE_SKINNY_NS")) : 0;
     static const int env_nw = getenv("MOE_SKINNY_NW") ? atoi(getenv("MOE_SKINNY_NW")) : 0;
