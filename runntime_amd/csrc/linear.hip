@@ -18,7 +18,7 @@
 namespace {
 
 constexpr int LCOLS = 64;   // columns per block (one per lane)
-constexpr int LKS = 64;     // K per slice
+constexpr int LKS = 32;     // K per slice
 constexpr int LRB = 16;     // rows per pass
 
 __global__ __launch_bounds__(LCOLS) void k_linear_partial(const float *__restrict__ x,
@@ -32,15 +32,30 @@ __global__ __launch_bounds__(LCOLS) void k_linear_partial(const float *__restric
   const int k0 = s * LKS, kl = min(LKS, K - k0);
   const bool col = n < N;
   float *out = part + (int64_t)s * T * N;
-  // The column's K slice in registers, every load issued at once.
+  // The column's K slice in registers, every load issued at once. The
+  // addresses are clamped into the matrix and the values past it zeroed,
+  // so no load sits under a branch.
   float wr[LKS];
+  const int nc = min(n, N - 1);
 #pragma unroll
-  for (int kk = 0; kk < LKS; kk++)
-    wr[kk] = (col && kk < kl) ? w[(int64_t)(k0 + kk) * N + n] : 0.f;
+  for (int kk = 0; kk < LKS; kk++) {
+    const float v = w[(int64_t)min(k0 + kk, K - 1) * N + nc];
+    wr[kk] = kk < kl ? v : 0.f;
+  }
   const int rows = min(LRB, T - r_first);
-  for (int i = threadIdx.x; i < LRB * LKS; i += LCOLS) {
-    const int r = i / LKS, kk = i % LKS;
-    xs[r][kk] = (r < rows && kk < kl) ? x[(int64_t)(r_first + r) * K + k0 + kk] : 0.f;
+  // x slab, every load issued before the first LDS store (a load-store
+  // pair per iteration waits out each load's latency in turn).
+  constexpr int PER = LRB * LKS / LCOLS;
+  float xv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = threadIdx.x + LCOLS * j, r = i / LKS, kk = i % LKS;
+    xv[j] = (r < rows && kk < kl) ? x[(int64_t)(r_first + r) * K + k0 + kk] : 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = threadIdx.x + LCOLS * j;
+    xs[i / LKS][i % LKS] = xv[j];
   }
   __syncthreads();
   if (!col) return;
@@ -66,8 +81,18 @@ __global__ void k_linear_reduce(const float *__restrict__ part, int S, const flo
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)T * N) return;
   const int n = (int)(i % N);
-  float v = part[i];
-  for (int s = 1; s < S; s++) v += part[(int64_t)s * T * N + i];
+  // Slices added in order, their loads issued 8 at a time.
+  const int64_t sl = (int64_t)T * N;
+  float v = 0.f;
+  int s = 0;
+  for (; s + 8 <= S; s += 8) {
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) q[j] = part[(s + j) * sl + i];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v = (s + j == 0) ? q[j] : v + q[j];
+  }
+  for (; s < S; s++) v = s == 0 ? part[i] : v + part[s * sl + i];
   if (bias) v += bias[n];
   if (addend) v += addend[i];
   y[i] = v;
