@@ -212,6 +212,40 @@ __device__ __forceinline__ void fold_logits(const float *partial, const float *b
   }
 }
 
+// fold_logits in two halves, so that a wavefront that takes several tokens
+// can issue the next token's loads before the current token's top-k.
+template <int NI, int FB>
+struct FoldLoads {
+  float v[NI][FB];
+};
+template <int NI, int FB>
+__device__ __forceinline__ void fold_load(const float *partial, int t, int J, int E, int lane,
+                                          FoldLoads<NI, FB> &L) {
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int e = min(lane + moe_dev::WAVE * i, E - 1);  // in bounds; lanes past E unused
+    const float *p = partial + (int64_t)t * J * E + e;
+#pragma unroll
+    for (int u = 0; u < FB; u++) L.v[i][u] = p[(int64_t)min(u, J - 1) * E];
+  }
+}
+// The same sum as fold_logits (chunk order, then + b) from loads already in
+// registers; J ≤ FB.
+template <int NI, int FB>
+__device__ __forceinline__ void fold_sum(const FoldLoads<NI, FB> &L, const float *b, int J, int E,
+                                         int lane, float (&vals)[NI]) {
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int e = lane + moe_dev::WAVE * i;
+    float s = L.v[i][0];
+#pragma unroll
+    for (int u = 1; u < FB; u++)
+      if (u < J) s = s + L.v[i][u];
+    if (b && e < E) s = s + b[e];
+    vals[i] = e < E ? s : -INFINITY;
+  }
+}
+
 // One wavefront per token: fold, top-k, route row.
 template <int NI, int FB>
 __global__ __launch_bounds__(256) void k_router_fold_topk(RouterArgs ra) {
@@ -246,15 +280,35 @@ __global__ __launch_bounds__(1024) void k_router_fold_topk_dispatch(RouterArgs r
   const int call = blockIdx.x;
   const int E = ra.E, k = ra.k, A = ra.T * ra.k;
   for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
-  for (int t = threadIdx.x / moe_dev::WAVE; t < ra.T; t += nwaves) {
-    const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-    const float *partial = ra.partial + call * ((int64_t)ra.T * J * E);
-    const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
-    float vals[NI];
-    fold_logits<NI, FB>(partial, b, t, J, E, lane, vals);
-    int id = wave_topk_route<NI>(vals, E, k, lane,
-                                 ra.route + call * ra.route_cs + (int64_t)t * 2 * k);
-    if (lane < k) sid[t * k + lane] = id;
+  const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
+  const float *partial = ra.partial + call * ((int64_t)ra.T * J * E);
+  const float *b = ra.b ? ra.b + call * ra.b_cs : nullptr;
+  // Two tokens' loads live at once: only while they take ≤ 64 registers.
+  if (NI * FB <= 32 && J <= FB) {
+    // Tokens t, t + nwaves, …: the next token's partials (its index
+    // clamped to the last token, so no load sits under a branch) are in
+    // flight during this token's top-k.
+    int t = threadIdx.x / moe_dev::WAVE;
+    FoldLoads<NI, FB> cur;
+    fold_load<NI, FB>(partial, min(t, ra.T - 1), J, E, lane, cur);
+    for (; t < ra.T; t += nwaves) {
+      FoldLoads<NI, FB> nxt;
+      fold_load<NI, FB>(partial, min(t + nwaves, ra.T - 1), J, E, lane, nxt);
+      float vals[NI];
+      fold_sum<NI, FB>(cur, b, J, E, lane, vals);
+      int id = wave_topk_route<NI>(vals, E, k, lane,
+                                   ra.route + call * ra.route_cs + (int64_t)t * 2 * k);
+      if (lane < k) sid[t * k + lane] = id;
+      cur = nxt;
+    }
+  } else {
+    for (int t = threadIdx.x / moe_dev::WAVE; t < ra.T; t += nwaves) {
+      float vals[NI];
+      fold_logits<NI, FB>(partial, b, t, J, E, lane, vals);
+      int id = wave_topk_route<NI>(vals, E, k, lane,
+                                   ra.route + call * ra.route_cs + (int64_t)t * 2 * k);
+      if (lane < k) sid[t * k + lane] = id;
+    }
   }
   __syncthreads();
   const int a = threadIdx.x;
