@@ -22,6 +22,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int WAVE = 64;
@@ -101,18 +103,37 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
 
   // Items: it = wave + AW·i → row it / G, head kvh·G + it % G.
   const int nitems = min(R, a.q_len - row0) * G;
-  for (int e = threadIdx.x; e < AW * AI * HP; e += blockDim.x) {
-    const int it = e / HP, x = e % HP;
-    float val = 0.f;
-    if (it < nitems && x < hd) {
-      const int r = row0 + it / G, h = kvh * G + it % G;
-      const int64_t qi = (int64_t)r * a.q_rs + (int64_t)h * hd + x;
-      val = a.rope_cos ? roped(q, qi, x, a.rope_cos[(int64_t)r * hd + x],
-                               a.rope_sin[(int64_t)r * hd + x])
-                       : ld(q, qi);
+  // Staging (q here, K and V per chunk below): 8 elements per thread at a
+  // time, their loads issued before the LDS stores, from indices clamped
+  // into the tensors (values past them zeroed), so no load sits under a
+  // branch; rope or not is one uniform choice around the whole loop. (A
+  // load and store per strided iteration waited out each load in turn.)
+  constexpr int NT = AW * WAVE;    // threads per block
+  constexpr int PER = AKC * HP / NT;  // = AW·AI·HP / NT: elements per thread
+  static_assert(AKC == AW * AI && PER % 8 == 0, "staging shape");
+  auto stage_q = [&](auto rope) {
+#pragma unroll
+    for (int b0 = 0; b0 < PER; b0 += 8) {
+      float qv[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int e = threadIdx.x + NT * (b0 + u), it = e / HP, x = e % HP;
+        const int itc = min(it, nitems - 1), xc = min(x, hd - 1);
+        const int r = row0 + itc / G, h = kvh * G + itc % G;
+        const int64_t qi = (int64_t)r * a.q_rs + (int64_t)h * hd + xc;
+        float val;
+        if constexpr (decltype(rope)::value)
+          val = roped(q, qi, xc, a.rope_cos[(int64_t)r * hd + xc], a.rope_sin[(int64_t)r * hd + xc]);
+        else
+          val = ld(q, qi);
+        qv[u] = (it < nitems && x < hd) ? val : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) qs[threadIdx.x + NT * (b0 + u)] = qv[u];
     }
-    qs[e] = val;
-  }
+  };
+  if (a.rope_cos) stage_q(std::true_type{});
+  else stage_q(std::false_type{});
 
   // The rows' key ranges.
   auto range = [&](int r, int &lo, int &hi) {
@@ -157,20 +178,37 @@ __global__ __launch_bounds__(AW *WAVE) void k_sdpa(AttnArgs a) {
 
   for (int c0 = blo; c0 <= bhi; c0 += AKC) {
     __syncthreads();  // the previous chunk's reads are done (and qs is written)
-    for (int e = threadIdx.x; e < AKC * HP; e += blockDim.x) {
-      const int j = e / HP, x = e % HP;
-      const int key = c0 + j;
-      float kv = 0.f, vv = 0.f;
-      if (key <= bhi && x < hd) {
-        const int64_t ki = (int64_t)key * a.k_rs + (int64_t)kvh * hd + x;
-        kv = a.rope_cos ? roped(k, ki, x, a.rope_cos[(int64_t)key * hd + x],
-                                a.rope_sin[(int64_t)key * hd + x])
-                        : ld(k, ki);
-        vv = ld(v, (int64_t)key * a.v_rs + (int64_t)kvh * hd + x);
+    auto stage_kv = [&](auto rope) {
+#pragma unroll
+      for (int b0 = 0; b0 < PER; b0 += 8) {
+        float kv[8], vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int e = threadIdx.x + NT * (b0 + u), j = e / HP, x = e % HP;
+          const int key = c0 + j;
+          const int kc = min(key, bhi), xc = min(x, hd - 1);  // c0 ≤ kc ≤ bhi < kv_len
+          const int64_t ki = (int64_t)kc * a.k_rs + (int64_t)kvh * hd + xc;
+          float kval;
+          if constexpr (decltype(rope)::value)
+            kval = roped(k, ki, xc, a.rope_cos[(int64_t)kc * hd + xc],
+                         a.rope_sin[(int64_t)kc * hd + xc]);
+          else
+            kval = ld(k, ki);
+          const float vval = ld(v, (int64_t)kc * a.v_rs + (int64_t)kvh * hd + xc);
+          const bool in = key <= bhi && x < hd;
+          kv[u] = in ? kval : 0.f;
+          vv[u] = in ? vval : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int e = threadIdx.x + NT * (b0 + u), j = e / HP, x = e % HP;
+          ks[j * KST + x] = kv[u];
+          vs[j * KST + x] = vv[u];
+        }
       }
-      ks[j * KST + x] = kv;
-      vs[j * KST + x] = vv;
-    }
+    };
+    if (a.rope_cos) stage_kv(std::true_type{});
+    else stage_kv(std::false_type{});
     __syncthreads();
     const int key = c0 + lane;
     float s[AI];
