@@ -63,7 +63,9 @@ def layer_flops(cfg):
 # valid for the default launch shape of each workload.
 TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md",
                     3: "k_expert_skinny_up_c3_batched_decode_traffic.md",
-                    "3-sequential": "k_expert_skinny_up_c3_decode_traffic.md"}
+                    "3-sequential": "k_expert_skinny_up_c3_decode_traffic.md",
+                    4: "k_expert_gemm_c4_prefill_traffic.md",
+                    5: "k_expert_gemm_c5_prefill_traffic.md"}
 
 
 def profiled_traffic(config, default_shape):
