@@ -416,6 +416,31 @@ def test_moe_layer_batched_equals_single_calls(T, cfg_id):
     assert_close(out[0], want, what="batched call 0")
 
 
+def test_moe_layer_batched_config3_shape():
+    """Batched calls at config 3's shape (f16 x, d = 2048, E = 64, k = 8,
+    I = 1408: the launch shape of config 3's bench line, with 4 KB+ weight
+    units) equal standalone moe_layer calls on each call's slices, bit for
+    bit."""
+    from runntime_amd.synth import make_weight_copies
+    cfg = CONFIGS[3]
+    C = 3
+    say(f"moe_layer_batched T={cfg.T} calls={C} {cfg.name}")
+    wc = make_weight_copies(cfg, C, seed=11, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn((C, cfg.T, cfg.d), generator=g, device=DEV).half()
+    res = torch.randn((C, cfg.T, cfg.d), generator=g, device=DEV)
+    for w in (wc.glu, wc.lin, wc.down):
+        w.bias.copy_(torch.randn(w.bias.shape, generator=g, device=DEV) * 0.1)
+    out, route = rt.moe_layer_batched(x, wc.router_w, wc.router_b, wc.glu, wc.lin, wc.down, res,
+                                      cfg.k)
+    for c in range(C):
+        o1, r1 = rt.moe_layer(x[c], wc.router_w[c], wc.router_b[c], _slice_weight(wc.glu, c),
+                              _slice_weight(wc.lin, c), _slice_weight(wc.down, c), res[c], cfg.k,
+                              return_route=True)
+        assert torch.equal(r1, route[c])
+        assert torch.equal(o1, out[c])
+
+
 def test_graph_replay_matches_eager():
     """A captured moe_layer_batched replays correctly several times, with
     eager work and synchronisation between the replays."""
