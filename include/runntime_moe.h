@@ -129,6 +129,15 @@ MOE_API int moe_ctx_set_stream(moe_ctx *ctx, void *stream);
 MOE_API int moe_ctx_reserve(moe_ctx *ctx, int T, int d, int I, int E, int k);
 /* As moe_ctx_reserve, for moe_layer_batched with up to `calls` calls. */
 MOE_API int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, int I, int E, int k);
+/* Pin (pin = 1) or unpin (pin = 0) the context's workspace: while pinned at
+ * least once, a call that needs a larger workspace fails with
+ * EXECUTION_FAILED instead of reallocating it, so graphs captured over the
+ * workspace keep a valid address. Pins nest; unpinning an unpinned context is
+ * INVALID_ARGUMENT. A call made while its stream is capturing never grows
+ * the workspace either (reserve before capture). No reference counterpart:
+ * the reference's BufferPool (src/core/gpu/bufferPool.ts:1-25) hands out
+ * buffers per dispatch and has no captured graphs. */
+MOE_API int moe_ctx_pin_workspace(moe_ctx *ctx, int pin);
 MOE_API int moe_ctx_destroy(moe_ctx *ctx);
 /* Wait for the context's stream; reports a device fault as EXECUTION_FAILED. */
 MOE_API int moe_sync(moe_ctx *ctx);
@@ -343,6 +352,48 @@ MOE_API int moe_weights_view(const moe_weights *h, moe_expert_weight *view);
 MOE_API int moe_weights_dispose(moe_weights *h);
 /* Disposes if needed and frees the handle itself. */
 MOE_API int moe_weights_release(moe_weights *h);
+
+/* ------------------------------------------------ executor plumbing (host)
+ *
+ * What a ruNNtime Executor backed by this library needs besides the ops
+ * (src/core/graph/evalCore.ts:14-43): the shape checks its op builders run,
+ * and device buffers to hand out, fill and read back. */
+
+/* A Value's metadata, as ValueMeta (src/core/graph/value.ts:17-24): the
+ * element count in units of dtype (u32 words for quantW) and the dims when
+ * the value has a logical shape (rank 0: none). */
+typedef enum moe_value_dtype {
+  MOE_VALUE_F32 = 0, MOE_VALUE_F16 = 1, MOE_VALUE_QUANTW = 2
+} moe_value_dtype;
+typedef struct moe_value_desc {
+  int dtype;       /* moe_value_dtype */
+  int rank;        /* number of dims, 0..4 */
+  int64_t dims[4];
+  int64_t elems;
+} moe_value_desc;
+
+/* checkExpertWeight (src/core/graph/ops/matmul.ts:274-315), host only, no
+ * context: the checks moeUp / moeDown run on one routed layer's weight
+ * {w, scales, bias} against its input's K (k_in) and the route of t tokens
+ * with `slots` ids per token (the reference's 4). INVALID_ARGUMENT with the
+ * reference's message on the first failed check; else n_out and
+ * experts_out (may be NULL) receive N and the expert count. */
+MOE_API int moe_check_expert_weight(const char *op, const moe_value_desc *w,
+                                    const moe_value_desc *scales, const moe_value_desc *bias,
+                                    const moe_value_desc *route, int64_t k_in, int64_t t,
+                                    int slots, int bits, int group_size, int64_t *n_out,
+                                    int64_t *experts_out);
+
+/* Device buffers on the context's device: the Executor's acquireOutput /
+ * releaseOutput (evalCore.ts:14-17), an upload (the reference's
+ * upload(), test/gpu.ts:73-83) and a Readback (evalCore.ts:38-43).
+ * Write and read are synchronous with the context's stream (they wait for
+ * the work queued before them). A zero-byte buffer is INVALID_ARGUMENT, as
+ * the reference's empty upload. */
+MOE_API int moe_buffer_alloc(moe_ctx *ctx, size_t bytes, void **out);
+MOE_API int moe_buffer_free(moe_ctx *ctx, void *ptr);
+MOE_API int moe_buffer_write(moe_ctx *ctx, void *dst, const void *host, size_t bytes);
+MOE_API int moe_buffer_read(moe_ctx *ctx, void *host, const void *src, size_t bytes);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,9 @@ EXPORTED = (
     "moe_layer_batched", "moe_ctx_reserve_batched", "moe_pack_quantw",
     "moe_weights_upload", "moe_weights_view", "moe_weights_dispose", "moe_weights_release",
     "moe_block", "moe_rmsnorm", "moe_matmul_gather", "moe_block_float", "moe_rope",
-    "moe_sdpa", "moe_linear", "moe_viterbi_decode", "moe_attention",
+    "moe_sdpa", "moe_linear", "moe_viterbi_decode", "moe_attention", "moe_ctx_pin_workspace",
+    "moe_check_expert_weight", "moe_buffer_alloc", "moe_buffer_free", "moe_buffer_write",
+    "moe_buffer_read",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine", "norm")
 
@@ -34,6 +36,12 @@ class CallStridesC(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int64) for n in (
         "x", "router_w", "router_b", "glu_w", "glu_scales", "glu_bias", "lin_w", "lin_scales",
         "lin_bias", "down_w", "down_scales", "down_bias", "residual", "route", "out")]
+
+
+class ValueDescC(ctypes.Structure):
+    """moe_value_desc: a Value's ValueMeta (dtype code, dims, elems)."""
+    _fields_ = [("dtype", ctypes.c_int), ("rank", ctypes.c_int), ("dims", ctypes.c_int64 * 4),
+                ("elems", ctypes.c_int64)]
 
 
 class ExpertWeightC(ctypes.Structure):
@@ -78,6 +86,15 @@ def load() -> ctypes.CDLL:
             "moe_layer_batched": ([P, I, ctypes.POINTER(CallStridesC), P, I, P, P, W, W, W, P, I,
                                    I, I, I, I, I, I, I, P, P], I),
             "moe_ctx_reserve_batched": ([P, I, I, I, I, I, I], I),
+            "moe_ctx_pin_workspace": ([P, I], I),
+            "moe_check_expert_weight": ([ctypes.c_char_p] + [ctypes.POINTER(ValueDescC)] * 4 +
+                                        [ctypes.c_int64, ctypes.c_int64, I, I, I,
+                                         ctypes.POINTER(ctypes.c_int64),
+                                         ctypes.POINTER(ctypes.c_int64)], I),
+            "moe_buffer_alloc": ([P, ctypes.c_size_t, ctypes.POINTER(P)], I),
+            "moe_buffer_free": ([P, P], I),
+            "moe_buffer_write": ([P, P, P, ctypes.c_size_t], I),
+            "moe_buffer_read": ([P, P, P, ctypes.c_size_t], I),
             "moe_prof_read": ([P, I, P, P], I),
             "moe_weights_upload": ([P, P, I, P, P, I, I, I, I, I, ctypes.POINTER(P)], I),
             "moe_weights_view": ([P, W], I),
@@ -129,3 +146,11 @@ def context(device: int, stream_handle: int) -> int:
             _ctxs[device] = ctx
     check(lib.moe_ctx_set_stream(ctx, stream_handle or MOE_NULL_STREAM))
     return ctx
+
+
+def pin_workspace(device: int, pin: bool) -> None:
+    """Pins (or unpins) the workspace of `device`'s context: while pinned, a
+    call that needs more workspace raises instead of moving it."""
+    lib = load()
+    ctx = context(device, 0)
+    check(lib.moe_ctx_pin_workspace(ctx, 1 if pin else 0))

@@ -662,12 +662,7 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     // (K = 2048 and 1408) measured NS = 1 faster at 2-16 calls per launch
     // (up 64-78% against 54-74% of HBM).
     const long waves_ns2 = (long)ea.calls * max_active * (MODE == MODE_UP ? ncg : (ncg + 1) / 2);
-    int ns = (waves_ns2 >= 2048 && ea.K < 1024) ? 2 : 1;
-    // Tuning overrides (MOE_SKINNY_NS = 1|2, MOE_SKINNY_NW = 1|2|4).
-    static const int env_ns = getenv("MOE_SKINNY_NS") ? atoi(getenv("MOE_SKINNY_NS")) : 0;
-    static const int env_nw = getenv("MOE_SKINNY_NW") ? atoi(getenv("MOE_SKINNY_NW")) : 0;
-    if (env_ns == 1 || env_ns == 2) ns = env_ns;
-    if (env_nw == 1 || env_nw == 2 || env_nw == 4) nw = env_nw;
+    const int ns = (waves_ns2 >= 2048 && ea.K < 1024) ? 2 : 1;
     if (MODE == MODE_UP && ns == 1 && nw == 1) nw = 2;  // glu/lin pairs
     const int gpw = (MODE == MODE_UP) ? 1 : ns;
     const int cg_per_block = (MODE == MODE_UP && ns == 1) ? nw / 2 : nw * gpw;
@@ -679,9 +674,7 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     const long streams = (long)ea.calls * max_active *
                          ((ncg + cg_per_block - 1) / cg_per_block) * nw;
     const int steps = (ea.K + 31) / 32;
-    int ks = (!grouped && steps % 2 == 0 && streams < 1024) ? 2 : 1;
-    static const int env_ks = getenv("MOE_SKINNY_KS") ? atoi(getenv("MOE_SKINNY_KS")) : 0;
-    if (env_ks == 1 || (env_ks == 2 && !grouped && steps % 2 == 0)) ks = env_ks;
+    const int ks = (!grouped && steps % 2 == 0 && streams < 1024) ? 2 : 1;
     dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw * ks);
     // Up parks one [4][64] floatx4 per stream (per pair when paired).
     const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
@@ -721,9 +714,8 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
 
 bool expert_uses_gemm(const ExpertArgs &ea) {
   // Prefill shapes (≥ 64 rows per expert on average): the grouped GEMM.
-  static const int env_gemm = getenv("MOE_GEMM") ? atoi(getenv("MOE_GEMM")) : -1;
   const int max_active = ea.E < ea.A ? ea.E : ea.A;
-  const bool want_gemm = env_gemm >= 0 ? env_gemm != 0 : ea.A >= 64 * max_active;
+  const bool want_gemm = ea.A >= 64 * max_active;
   return ea.calls == 1 && want_gemm && gemm_eligible(ea);
 }
 

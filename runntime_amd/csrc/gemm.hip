@@ -12,18 +12,19 @@
 // bias.
 //
 // Tiles: 128 rows × 128 weight units (512 columns) per block, eight
-// wavefronts as 2 (rows) × 4 (units), each owning 64 rows × 32 units: 2 × 4
-// v_mfma_f32_32x32x16_f16 tiles (128 accumulators, two wavefronts per
-// SIMD). The block's units come from two sources of 64 units each: up takes
-// the same 64 units (256 outputs) of glu and of lin, down takes 128
-// consecutive units of its one weight (512 outputs). An up wavefront's 32
-// units are 16 of glu (lanes 0-15 of a half) and the same 16 of lin (lanes
-// 16-31), so the SwiGLU pairs lanes 16 apart. Each converted weight
-// fragment feeds two MFMAs: the int8 → f16 conversion (VALU) is what bounds
-// a wavefront tile one MFMA tall. A 128 × 512 tile per CU
-// is what the register file holds; its operands (16 KB of f16 A and 32 KB of
-// int8 weights per 64 k) come through L2, whose bandwidth and latency bound
-// this kernel together with the MFMAs.
+// wavefronts, two per SIMD, 128 accumulators each. The block's units come
+// from two sources of 64 units each: up takes the same 64 units (256
+// outputs) of glu and of lin, down takes 128 consecutive units of its one
+// weight (512 outputs). Two wavefront shapes:
+//  - f16 A (up with f16 x): each wavefront takes all 128 rows and 16 slots
+//    (8 glu units and the same 8 lin units) with two of each unit's four
+//    columns per lane: 4 × 2 v_mfma_f32_32x32x16_f16 tiles, so one
+//    converted weight fragment feeds four MFMAs. The SwiGLU pairs lanes 16
+//    apart.
+//  - f32 or f16-pair A (down, up with f32 x): 2 (row halves) × 4 (unit
+//    groups), 64 rows × 32 units with all four columns each: 2 × 4 tiles.
+// A tile's operands (16 KB of int8 weights and 8 or 16 KB of A per 32 k)
+// come through L2.
 //
 // Weights go to LDS as the quantW words are: 16-byte tiles of 4 columns × 4
 // k, [column][k] bytes, so dword c of a tile is column c's four k values.
@@ -35,12 +36,17 @@
 // unchanged. int8 → f16 is exact (|q| ≤ 127).
 //
 // Loads go straight from global memory to LDS (buffer_load … lds): a ring of
-// STAGES steps, STAGES − 1 of them in flight while one is computed; no
-// staging registers and no LDS stores. Each step: wait for this wavefront's
-// loads of the step, barrier (all wavefronts' loads landed, and the previous
-// step's LDS reads are done), issue the loads of the step STAGES − 1 ahead
-// into the slot just freed, compute. The waits are explicit vmcnt counts:
-// the compiler does not track loads that write LDS.
+// STAGES 32-k steps; no staging registers and no LDS stores. A workgroup
+// barrier comes every step, or every second step when a tile's step count
+// is even (PAIR): at the barrier every wavefront has read the slots of the
+// steps it just used, so their loads for STAGES steps ahead may go out. A
+// wavefront issues those loads spread between its MFMA groups rather than
+// all at once after the barrier: when every wavefront issues its DMA burst
+// at the same moment their issue stalls together and the matrix cores idle
+// (measured: the memory-only and compute-only variants of the loop took
+// 0.53 ms each at config 4's up shape, together 0.94 ms with the burst).
+// The waits are explicit vmcnt counts: the compiler does not track loads
+// that write LDS.
 //
 // LDS positions are chosen so that the fragment reads hit distinct banks
 // (SQ_LDS_BANK_CONFLICT reads 0). Rows of 128 bytes (a weight slot's 8
@@ -157,7 +163,14 @@ __device__ __forceinline__ int sw8w(int s) { return sw8(s) ^ (TALL ? (s >> 6) & 
 // vmcnt waits order them. (The compiler's own waits for other vector loads
 // only count its own loads and so can only wait longer with these in
 // flight.) M0 holds the LDS address; nothing else in this kernel uses M0.
+__device__ __forceinline__ i32x4 uniform4(i32x4 v) {
+  return i32x4{__builtin_amdgcn_readfirstlane(v[0]), __builtin_amdgcn_readfirstlane(v[1]),
+               __builtin_amdgcn_readfirstlane(v[2]), __builtin_amdgcn_readfirstlane(v[3])};
+}
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, int soff, uint32_t lds_addr) {
+  rsrc = uniform4(rsrc);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :: "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr) : "memory");
 }
@@ -168,6 +181,9 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void *base, uint32_t bytes) {
 
 // The same for 4 bytes per lane (LDS at lds_addr + 4·lane).
 __device__ __forceinline__ void dma4(i32x4 rsrc, uint32_t voff, int soff, uint32_t lds_addr) {
+  rsrc = uniform4(rsrc);
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  lds_addr = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds"
                :: "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr) : "memory");
 }
@@ -196,7 +212,7 @@ struct Tile {
 };
 
 // OPAIR (up): write act as f16 pairs. AT = f16pair (down): read them.
-template <int MODE, typename AT, bool OPAIR>
+template <int MODE, typename AT, bool OPAIR, bool PAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_expert_gemm(GemmArgs p) {
   constexpr bool SPLIT = sizeof(AT) == 4;
@@ -374,13 +390,15 @@ void k_expert_gemm(GemmArgs p) {
     }
     return P;
   };
-  auto issue = [&](const Params &P, int ks, int stage) {
+  // Load instruction q of step ks into slot `stage`: q < 2 weights, else A.
+  auto issue_q = [&](const Params &P, int ks, int stage, int q) {
     const uint32_t st = lds0 + stage * STAGE;
+    if (q < 2) dma16(P.wr, P.woff[q], ks * (TPS * 16), st + (2 * wave + q) * 1024);
+    else dma16(ar, P.aoff[q - 2], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + q - 2) * 1024);
+  };
+  auto issue = [&](const Params &P, int ks, int stage) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) dma16(P.wr, P.woff[i], ks * (TPS * 16), st + (2 * wave + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < AI; i++)
-      dma16(ar, P.aoff[i], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + i) * 1024);
+    for (int q = 0; q < LOADS; q++) issue_q(P, ks, stage, q);
   };
 
   floatx16 acc[RT][CT];
@@ -423,41 +441,57 @@ void k_expert_gemm(GemmArgs p) {
       }
     }
   };
-  // The MFMAs of one slice: column c outer, so converting column c + 1
-  // overlaps the MFMAs of column c.
-  auto mfma_slice = [&](const Frags &F, int kk) {
+  // The MFMAs of one slice (when `live`), column c outer: the conversion of
+  // column c + 1 is placed before the MFMAs of column c, so it overlaps
+  // them. After column c's MFMAs, hook(c) issues the ring loads scheduled
+  // there: the loads of a step are spread over the MFMA groups instead of
+  // leaving every wavefront at once after the barrier (a burst of DMA
+  // instructions from all wavefronts stalls their issue together, and the
+  // matrix cores with it).
+  // RTL: the wavefront's live 32-row tiles (compile time); live: a runtime
+  // switch for the whole slice (the split shapes keep one loop copy).
+  auto mfma_slice = [&](const Frags &F, int kk, auto rtl, bool live, auto &&hook) {
+    constexpr int RTL = decltype(rtl)::value;
     constexpr int PL = SPLIT ? 2 : 1;
     half8 af[RT][PL];
+    half8 bf[CT];
+    if (RTL > 0 && live) {
 #pragma unroll
-    for (int i = 0; i < RT; i++) {
-      if constexpr (PAIRS) {
-        const u32x4 c0 = F.a[kk][i][0], c1 = F.a[kk][i][1];
-        af[i][0] = __builtin_bit_cast(half8, u32x4{c0[0], c0[2], c1[0], c1[2]});
-        af[i][1] = __builtin_bit_cast(half8, u32x4{c0[1], c0[3], c1[1], c1[3]});
-      } else if constexpr (SPLIT) {
-        const floatx4 v0 = __builtin_bit_cast(floatx4, F.a[kk][i][0]);
-        const floatx4 v1 = __builtin_bit_cast(floatx4, F.a[kk][i][1]);
+      for (int i = 0; i < RT; i++) {
+        if constexpr (PAIRS) {
+          const u32x4 c0 = F.a[kk][i][0], c1 = F.a[kk][i][1];
+          af[i][0] = __builtin_bit_cast(half8, u32x4{c0[0], c0[2], c1[0], c1[2]});
+          af[i][1] = __builtin_bit_cast(half8, u32x4{c0[1], c0[3], c1[1], c1[3]});
+        } else if constexpr (SPLIT) {
+          const floatx4 v0 = __builtin_bit_cast(floatx4, F.a[kk][i][0]);
+          const floatx4 v1 = __builtin_bit_cast(floatx4, F.a[kk][i][1]);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const float x = j < 4 ? v0[j] : v1[j - 4];
-          const _Float16 xh = (_Float16)x;
-          af[i][0][j] = xh;
-          af[i][PL - 1][j] = (_Float16)(x - (float)xh);
+          for (int j = 0; j < 8; j++) {
+            const float x = j < 4 ? v0[j] : v1[j - 4];
+            const _Float16 xh = (_Float16)x;
+            af[i][0][j] = xh;
+            af[i][PL - 1][j] = (_Float16)(x - (float)xh);
+          }
+        } else {
+          af[i][0] = __builtin_bit_cast(half8, F.a[kk][i][0]);
         }
-      } else {
-        af[i][0] = __builtin_bit_cast(half8, F.a[kk][i][0]);
       }
+      bf[0] = cvt_i8x8(F.w[kk][0][0], F.w[kk][1][0]);
     }
 #pragma unroll
     for (int c = 0; c < CT; c++) {
-      const half8 bf = cvt_i8x8(F.w[kk][0][c], F.w[kk][1][c]);
+      if (RTL > 0 && live) {
+        if (c + 1 < CT) bf[c + 1] = cvt_i8x8(F.w[kk][0][c + 1], F.w[kk][1][c + 1]);
 #pragma unroll
-      for (int pl = 0; pl < PL; pl++)
+        for (int pl = 0; pl < PL; pl++)
 #pragma unroll
-        for (int i = 0; i < RT; i++)
-          acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][pl], bf, acc[i][c], 0, 0, 0);
+          for (int i = 0; i < RTL; i++)
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][pl], bf[c], acc[i][c], 0, 0, 0);
+      }
+      hook(c);
     }
   };
+  auto no_loads = [](int) {};
 
   // ---- epilogue of tile T from LDS buffer `sel`. acc[i][c][r]: row
   // 64wm + 32i + 8(r/4) + 4h + r%4, column cb + c of this lane's unit. Outputs go
@@ -592,15 +626,28 @@ void k_expert_gemm(GemmArgs p) {
   block_barrier();
   Params pc = make_params(cur, 0), pn = pc;
   if (ntiles > 1) nxt = tile_at(start + bx);
+  // PAIR: one barrier per two steps. At the barrier in the middle of an
+  // even step ks every wavefront has read all of steps ks − 1 and ks (their
+  // fragments are in registers or consumed), so those two slots take steps
+  // ks + STAGES − 1 and ks + STAGES; the wait covers steps ks + 1 and
+  // ks + 2, whose fragments are read before the next barrier. The prologue
+  // loads STAGES − 1 steps.
+  constexpr int PRO = PAIR ? STAGES - 1 : STAGES;
 #pragma unroll
-  for (int s = 0; s < STAGES; s++) issue(pc, cur.kb + s, s);
-  WAIT_VMCNT((STAGES - 1) * LOADS);  // step 0
+  for (int s = 0; s < PRO; s++) issue(pc, cur.kb + s, s);
+  WAIT_VMCNT((PRO - 1) * LOADS);  // step 0
   block_barrier();
   Frags f;
   read_frags(f, 0, 0);
   read_frags(f, 0, 1);
-  const int tile_step = ksteps - 2 * STAGES;  // ≥ STAGES − 1 (checked on the host)
-  const int param_step = ksteps - STAGES - 1;
+  // Row map and constants of the next tile: loaded at tile_step, covered by
+  // the wait of the barrier before param_step, where its load parameters are
+  // made (the step of its first ring load). Both are even with PAIR.
+  const int tile_step = PAIR ? ksteps - 2 * STAGES + 2 : ksteps - 2 * STAGES;
+  const int param_step = PAIR ? ksteps - STAGES : ksteps - STAGES - 1;
+  // Ring loads issued after the awaited ones at a barrier.
+  constexpr int P_BASE = PAIR ? (STAGES - 4) * LOADS : BASE_WAIT;
+  constexpr int P_STORE = P_BASE + STORES < 63 ? P_BASE + STORES : 63;
   int stage = 0;  // slot of the step being computed
   for (int j = 0; j < ntiles; j++) {
     const bool has_next = j + 1 < ntiles;
@@ -609,35 +656,114 @@ void k_expert_gemm(GemmArgs p) {
     const int wu = MODE == MODE_UP ? cur.U0 + UPW * ug
                    : TALL          ? (wave < 4 ? cur.U0 : cur.U1) + 16 * (wave & 3)
                                    : (wn < 2 ? cur.U0 : cur.U1) + 32 * (wn & 1);
-    // Uniform: waves with no unit below N or no row in the tile skip the MFMAs.
-    const bool live = wu < N4 && 64 * wm < cur.rows;
+    // Uniform: the wavefront's 32-row tiles with a row of the tile (0 when
+    // it has no unit below N); the MFMAs of the others are skipped (the
+    // last M-tile of an expert is partial).
+    const int rt_live = wu >= N4 ? 0 : min(RT, max(0, (cur.rows - 64 * wm + 31) >> 5));
+    const bool live = TALL || rt_live > 0;
 #pragma unroll
     for (int i = 0; i < RT; i++)
 #pragma unroll
       for (int c = 0; c < CT; c++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][c][r] = 0.f;
-    for (int ks = 0; ks < ksteps; ks++) {
-      if (live) mfma_slice(f, 0);
+    // Ring loads of step a ≥ ksteps are the next tile's, or re-read the last
+    // step past the last tile, so every barrier issues the same count.
+    // The loads a barrier frees slots for: steps a0 (slot s0) and, with
+    // PAIR, a1 (slot s1), each resolved at the barrier to a step of the
+    // current tile (nx false) or of the next (nx true). Load j of the NL =
+    // LOADS (or 2·LOADS) goes after MFMA group j·NG / NL of the NG = CT (or
+    // 2·CT) groups that follow the barrier: slice 1 of this step and, with
+    // PAIR, slice 0 of the next.
+    int k0 = 0, s0 = 0, k1 = 0, s1 = 0;
+    bool nx0 = false, nx1 = false;
+    auto resolve = [&](int a, int &kstep, bool &nx) {
+      nx = a >= ksteps && has_next;
+      kstep = a < ksteps ? cur.kb + a : has_next ? nxt.kb + a - ksteps : cur.kb + ksteps - 1;
+    };
+    auto issue_sel = [&](bool nx, int kstep, int slot, int q) {
+      Params P;
+      P.wr = nx ? pn.wr : pc.wr;
+#pragma unroll
+      for (int i = 0; i < 2; i++) P.woff[i] = nx ? pn.woff[i] : pc.woff[i];
+#pragma unroll
+      for (int i = 0; i < AI; i++) P.aoff[i] = nx ? pn.aoff[i] : pc.aoff[i];
+      issue_q(P, kstep, slot, q);
+    };
+    constexpr int NL = PAIR ? 2 * LOADS : LOADS;
+    constexpr int NG = PAIR ? 2 * CT : CT;
+    auto loads_at = [&](int g) {
+#pragma unroll
+      for (int jl = 0; jl < NL; jl++)
+        if (jl * NG / NL == g) {
+          if (jl < LOADS) issue_sel(nx0, k0, s0, jl);
+          else issue_sel(nx1, k1, s1, jl - LOADS);
+        }
+    };
+    // One step; BAR: the step has the barrier (every step without PAIR,
+    // the even ones with it).
+    auto step = [&](int ks, auto bar, auto rtl) {
+      constexpr bool BAR = decltype(bar)::value;
+      if (PAIR && !BAR) mfma_slice(f, 0, rtl, live, [&](int c) { loads_at(CT + c); });
+      else mfma_slice(f, 0, rtl, live, no_loads);
       __builtin_amdgcn_sched_barrier(0);
       // ---- mid-step
-      if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(STORE_WAIT);
-      else if (has_next && ks > tile_step && ks <= tile_step + STAGES - 2) WAIT_VMCNT(BASE_WAIT + TILE_LOADS);
-      else WAIT_VMCNT(BASE_WAIT);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's LDS reads done
-      block_barrier();
-      if (has_next && ks == tile_step) issue_tile(nxt, sel ^ 1);
-      if (has_next && ks == param_step) pn = make_params(nxt, sel ^ 1);
-      const int ahead = ks + STAGES;
-      if (ahead < ksteps) issue(pc, cur.kb + ahead, stage);
-      else if (has_next) issue(pn, nxt.kb + ahead - ksteps, stage);
-      else issue(pc, cur.kb + ksteps - 1, stage);
+      if constexpr (!PAIR) {
+        if (j > 0 && ks <= STAGES - 2) WAIT_VMCNT(STORE_WAIT);
+        else if (has_next && ks > tile_step && ks <= tile_step + STAGES - 2) WAIT_VMCNT(BASE_WAIT + TILE_LOADS);
+        else WAIT_VMCNT(BASE_WAIT);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's LDS reads done
+        block_barrier();
+        if (has_next && ks == tile_step) issue_tile(nxt, sel ^ 1);
+        if (has_next && ks == param_step) pn = make_params(nxt, sel ^ 1);
+        resolve(ks + STAGES, k0, nx0);
+        s0 = stage;
+      } else if constexpr (BAR) {
+        // Younger than the awaited loads (issued after the barrier of step
+        // ks + 2 − STAGES): the previous tile's stores while that barrier
+        // was in the previous tile, the next tile's row map and constants
+        // when they were loaded at a barrier between.
+        if (j > 0 && ks <= STAGES - 4) WAIT_VMCNT(P_STORE);
+        else if (has_next && ks >= tile_step + 2 && ks <= tile_step + STAGES - 4) WAIT_VMCNT(P_BASE + TILE_LOADS);
+        else WAIT_VMCNT(P_BASE);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        block_barrier();
+        if (has_next && ks == tile_step) issue_tile(nxt, sel ^ 1);
+        if (has_next && ks == param_step) pn = make_params(nxt, sel ^ 1);
+        resolve(ks + STAGES - 1, k0, nx0);
+        s0 = stage == 0 ? STAGES - 1 : stage - 1;
+        resolve(ks + STAGES, k1, nx1);
+        s1 = stage;
+      }
       stage = stage + 1 == STAGES ? 0 : stage + 1;
       read_frags(f, stage, 0);  // next step (the next tile's first after a tile's last)
       __builtin_amdgcn_sched_barrier(0);
-      if (live) mfma_slice(f, 1);
+      if (BAR) mfma_slice(f, 1, rtl, live, loads_at);
+      else mfma_slice(f, 1, rtl, live, no_loads);
       __builtin_amdgcn_sched_barrier(0);
       read_frags(f, stage, 1);
+    };
+    auto kloop = [&](auto rtl) {
+      if constexpr (PAIR) {
+        for (int ks = 0; ks < ksteps; ks += 2) {
+          step(ks, std::true_type(), rtl);
+          step(ks + 1, std::false_type(), rtl);
+        }
+      } else {
+        for (int ks = 0; ks < ksteps; ks++) step(ks, std::true_type(), rtl);
+      }
+    };
+    // TALL wavefronts (all 128 rows) skip the dead row tiles of a partial
+    // tile; the 64-row wavefronts of the split shapes only skip a tile half
+    // with no row (more loop copies spill their registers).
+    if constexpr (TALL) {
+      if (rt_live >= 4) kloop(std::integral_constant<int, 4>());
+      else if (rt_live == 3) kloop(std::integral_constant<int, 3>());
+      else if (rt_live == 2) kloop(std::integral_constant<int, 2>());
+      else if (rt_live == 1) kloop(std::integral_constant<int, 1>());
+      else kloop(std::integral_constant<int, 0>());
+    } else {
+      kloop(std::integral_constant<int, RT>());
     }
     epilogue(cur, wu, sel);
     if (has_next) {
@@ -650,6 +776,7 @@ void k_expert_gemm(GemmArgs p) {
   // before the workgroup's LDS is released.
   WAIT_VMCNT(0);
 }
+
 
 }  // namespace
 
@@ -741,23 +868,30 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   // Dispatch-order act (the fused layer, both products here) is stored as
   // f16 pairs: up writes them, down reads them.
   const bool pairs = ea.dispatch_order != 0;
+  // Paired steps (one barrier per 64 k) when each part has an even number
+  // of steps.
+  const bool pair = p.kpart % 2 == 0;
+#define LAUNCH_P(M_, AT_, OP_)                                                            \
+  do {                                                                                    \
+    if (pair) hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true>), grid, block, 0, s, p); \
+    else hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, false>), grid, block, 0, s, p);  \
+  } while (0)
   if (ea.mode == MODE_UP) {
     if (ea.a_dtype == MOE_F16) {
-      if (pairs) hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((k_expert_gemm<MODE_UP, _Float16, false>), grid, block, 0, s, p);
+      if (pairs) LAUNCH_P(MODE_UP, _Float16, true);
+      else LAUNCH_P(MODE_UP, _Float16, false);
     } else {
-      if (pairs) hipLaunchKernelGGL((k_expert_gemm<MODE_UP, float, true>), grid, block, 0, s, p);
-      else hipLaunchKernelGGL((k_expert_gemm<MODE_UP, float, false>), grid, block, 0, s, p);
+      if (pairs) LAUNCH_P(MODE_UP, float, true);
+      else LAUNCH_P(MODE_UP, float, false);
     }
   } else if (pairs) {
     if (ea.a_dtype != MOE_F32)
       return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: dispatch-order act must be f32");
-    hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, f16pair, false>), grid, block, 0, s, p);
+    LAUNCH_P(MODE_DOWN, f16pair, false);
   } else {
-    if (ea.a_dtype == MOE_F16)
-      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, _Float16, false>), grid, block, 0, s, p);
-    else
-      hipLaunchKernelGGL((k_expert_gemm<MODE_DOWN, float, false>), grid, block, 0, s, p);
+    if (ea.a_dtype == MOE_F16) LAUNCH_P(MODE_DOWN, _Float16, false);
+    else LAUNCH_P(MODE_DOWN, float, false);
   }
+#undef LAUNCH_P
   return 0;
 }

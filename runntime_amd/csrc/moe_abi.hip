@@ -139,6 +139,21 @@ extern "C" int moe_ctx_set_stream(moe_ctx *ctx, void *stream) {
 
 int moe_ws_ensure(moe_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->ws_size) return MOE_OK;
+  // A graph captured over the workspace holds its address: never move it
+  // while pinned, nor inside a capture (the synchronize and the allocation
+  // below are not capturable).
+  if (ctx->ws_pins > 0)
+    return moe_fail(MOE_EXECUTION_FAILED,
+                    "workspace is pinned (captured graphs use it) and holds " +
+                        std::to_string(ctx->ws_size) + " bytes; this call needs " +
+                        std::to_string(bytes) + ": reserve before pinning");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  MOE_HIP_CHECK(hipStreamIsCapturing(ctx->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return moe_fail(MOE_EXECUTION_FAILED,
+                    "workspace of " + std::to_string(ctx->ws_size) + " bytes is too small for a "
+                    "call inside a stream capture (needs " + std::to_string(bytes) +
+                    "): reserve before capturing");
   // Work already queued may still read the old workspace.
   MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   if (ctx->ws) MOE_HIP_CHECK(hipFree(ctx->ws));
@@ -147,6 +162,19 @@ int moe_ws_ensure(moe_ctx *ctx, size_t bytes) {
   size_t want = bytes + bytes / 4;
   MOE_HIP_CHECK(hipMalloc((void **)&ctx->ws, want));
   ctx->ws_size = want;
+  return MOE_OK;
+}
+
+extern "C" int moe_ctx_pin_workspace(moe_ctx *ctx, int pin) {
+  int rc = check_ctx(ctx, "moe_ctx_pin_workspace");
+  if (rc) return rc;
+  if (pin) {
+    ctx->ws_pins++;
+  } else {
+    if (ctx->ws_pins == 0)
+      return moe_fail(MOE_INVALID_ARGUMENT, "moe_ctx_pin_workspace: workspace is not pinned");
+    ctx->ws_pins--;
+  }
   return MOE_OK;
 }
 
@@ -1003,4 +1031,80 @@ extern "C" int moe_weights_release(moe_weights *h) {
   int rc = moe_weights_dispose(h);
   delete h;
   return rc;
+}
+
+// ------------------------------------------------- executor plumbing (host)
+
+// checkExpertWeight (src/core/graph/ops/matmul.ts:274-315): the same checks
+// in the same order with the same messages, which callers match by regex.
+extern "C" int moe_check_expert_weight(const char *op_c, const moe_value_desc *w,
+                                       const moe_value_desc *scales, const moe_value_desc *bias,
+                                       const moe_value_desc *route, int64_t k, int64_t t,
+                                       int slots, int bits, int group_size, int64_t *n_out,
+                                       int64_t *experts_out) {
+  const std::string op = op_c ? op_c : "moe";
+  if (!w || !scales || !bias || !route)
+    return moe_fail(MOE_INVALID_ARGUMENT, op + ": NULL value descriptor");
+  REQUIRE(bits == 8 || bits == 4, op + ": bits must be 8 or 4, got " + S(bits));
+  REQUIRE(k > 0 && w->dtype == MOE_VALUE_QUANTW && w->rank == 2 && w->dims[0] % k == 0,
+          op + ": w must be a quantW [E·" + S(k) + ", N] weight");
+  const int64_t r = w->dims[0], n = w->dims[1];
+  const int64_t experts = r / k;
+  // (r·n·bits)/32 as the reference computes it; a fraction never matches.
+  REQUIRE((r * n * bits) % 32 == 0 && w->elems == r * n * bits / 32,
+          op + ": quantW weight elems " + S(w->elems) + " != rows·cols·" + S(bits) + "/32");
+  REQUIRE(k % 4 == 0 && n % 4 == 0,
+          op + ": K " + S(k) + " and N " + S(n) + " must be multiples of 4");
+  REQUIRE(group_size > 0 && group_size % 4 == 0 && k % group_size == 0,
+          op + ": groupSize " + S(group_size) + " must be a multiple of 4 that divides K " + S(k));
+  REQUIRE(scales->dtype == MOE_VALUE_F32 && scales->elems == experts * k * n / group_size,
+          op + ": scales must be f32 [" + S(experts * k / group_size) + ", " + S(n) + "]");
+  REQUIRE(bias->dtype == MOE_VALUE_F32 && bias->elems == experts * n,
+          op + ": bias must be f32 [" + S(experts) + ", " + S(n) + "]");
+  REQUIRE(route->dtype == MOE_VALUE_F32 && route->rank >= 2 && route->dims[0] == t &&
+              route->dims[1] == 2 * (int64_t)slots,
+          op + ": route must be topk's f32 [" + S(t) + ", " + S(2 * (int64_t)slots) + "] output");
+  if (n_out) *n_out = n;
+  if (experts_out) *experts_out = experts;
+  return MOE_OK;
+}
+
+extern "C" int moe_buffer_alloc(moe_ctx *ctx, size_t bytes, void **out) {
+  int rc = check_ctx(ctx, "moe_buffer_alloc");
+  if (rc) return rc;
+  REQUIRE(out, "moe_buffer_alloc: out is NULL");
+  REQUIRE(bytes > 0, "upload: the shape has no elements");
+  *out = nullptr;
+  MOE_HIP_CHECK(hipMalloc(out, bytes));
+  return MOE_OK;
+}
+
+extern "C" int moe_buffer_free(moe_ctx *ctx, void *ptr) {
+  int rc = check_ctx(ctx, "moe_buffer_free");
+  if (rc) return rc;
+  if (!ptr) return MOE_OK;
+  // Work queued on the context's stream may still use the buffer.
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  MOE_HIP_CHECK(hipFree(ptr));
+  return MOE_OK;
+}
+
+extern "C" int moe_buffer_write(moe_ctx *ctx, void *dst, const void *host, size_t bytes) {
+  int rc = check_ctx(ctx, "moe_buffer_write");
+  if (rc) return rc;
+  REQUIRE(dst && host, "moe_buffer_write: NULL pointer");
+  REQUIRE(bytes > 0, "upload: the shape has no elements");
+  MOE_HIP_CHECK(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  return MOE_OK;
+}
+
+extern "C" int moe_buffer_read(moe_ctx *ctx, void *host, const void *src, size_t bytes) {
+  int rc = check_ctx(ctx, "moe_buffer_read");
+  if (rc) return rc;
+  REQUIRE(src && host, "moe_buffer_read: NULL pointer");
+  if (bytes == 0) return MOE_OK;
+  MOE_HIP_CHECK(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  MOE_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  return MOE_OK;
 }

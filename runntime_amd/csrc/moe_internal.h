@@ -39,6 +39,7 @@ struct moe_ctx {
   hipStream_t own_stream = nullptr;  // created by the context
   char *ws = nullptr;                // device workspace
   size_t ws_size = 0;
+  int ws_pins = 0;                   // > 0: the workspace must not move
   bool disposed = false;
   bool prof_on = false;
   std::vector<ProfRecord> prof_pending;  // recorded, not yet resolved

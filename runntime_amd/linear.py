@@ -33,6 +33,17 @@ class Linear:
     bits: int = 0
     group_size: int = 0
 
+    def __post_init__(self):
+        w, b = self.weight, self.bias
+        if (w.dtype != torch.float32 or tuple(w.shape) != (self.in_features, self.out_features)
+                or not w.is_contiguous()):
+            raise ValueError(f"Linear: weight must be contiguous f32 [{self.in_features}, "
+                             f"{self.out_features}], got {w.dtype} {list(w.shape)}")
+        if b is not None and (b.dtype != torch.float32 or tuple(b.shape) != (self.out_features,)
+                              or not b.is_contiguous()):
+            raise ValueError(f"Linear: bias must be contiguous f32 [{self.out_features}], got "
+                             f"{b.dtype} {list(b.shape)}")
+
     @staticmethod
     def from_torch_layout(w_out_in: np.ndarray, bias: Optional[np.ndarray], device) -> "Linear":
         """A float checkpoint weight [out, in] (transposed once, as the
@@ -74,6 +85,8 @@ class Linear:
                                    or tuple(addend.shape) != (t, self.out_features)):
             raise ValueError(f"Linear: addend must be f32 [{t}, {self.out_features}]")
         x = x.contiguous()
+        if addend is not None:
+            addend = addend.contiguous()  # the kernel reads it as dense rows
         dev = _device_of(x, self.weight, *(a for a in (self.bias, addend) if a is not None))
         out = torch.empty((t, self.out_features), dtype=torch.float32, device=dev)
         lib = _lib.load()

@@ -81,7 +81,20 @@ class AttnBlock:
         from . import _lib
         from .core import _ctx, _xdtype, rmsNorm
         t = x.shape[0]
+        # moe_attention reads cos/sin rows 0..T-1 of 64 columns, 14 sinks and
+        # qkv as dense [T, 1152] rows: check what the pointers cannot say.
+        for name, tab in (("cos", cos), ("sin", sin)):
+            if (tab.dtype != torch.float32 or tab.dim() != 2 or tab.shape[0] < t
+                    or tab.shape[1] != HEAD or not tab.is_contiguous() or tab.device != x.device):
+                raise ValueError(f"AttnBlock: {name} must be a contiguous f32 [>= {t}, {HEAD}] "
+                                 f"table on {x.device}, got {tab.dtype} {list(tab.shape)} on "
+                                 f"{tab.device}")
+        if (self.sinks.dtype != torch.float32 or tuple(self.sinks.shape) != (Q_HEADS,)
+                or not self.sinks.is_contiguous() or self.sinks.device != x.device):
+            raise ValueError(f"AttnBlock: sinks must be a contiguous f32 [{Q_HEADS}] on {x.device}")
         qkv = self.qkv.forward(rmsNorm(x, self.norm_w, RMS_EPS))            # [T, 1152] f32
+        if tuple(qkv.shape) != (t, K_OFF + 2 * KV_HEADS * HEAD) or not qkv.is_contiguous():
+            raise ValueError(f"AttnBlock: qkv projection gave {list(qkv.shape)}")
         # rope(q), rope(k) and the banded sdpa in one kernel (moe_attention)
         attn = torch.empty((t, K_OFF), dtype=qkv.dtype, device=qkv.device)
         _lib.check(_lib.load().moe_attention(
@@ -131,10 +144,10 @@ class GraphedForward:
     The library's context workspace grows by reallocation. A graph holds
     the workspace address it was captured with, so every capture follows an
     eager forward at the longest length (the workspace each op plans grows
-    with the rows, so the longest length's covers all). Calls of other work
-    on the same device that need a larger workspace would reallocate it
-    under the graphs: run them before building this, or on another
-    device."""
+    with the rows, so the longest length's covers all), and the workspace is
+    pinned while the graphs live: a later call on the same device that needs
+    a larger workspace raises EXECUTION_FAILED instead of moving it under
+    the graphs. close() (or dropping the object) releases the pin."""
 
     def __init__(self, model: "PrivacyFilterModel", lengths):
         self.model = model
@@ -156,6 +169,25 @@ class GraphedForward:
                 out = self._body(x_in, cos, sin)
             self.graphs[t] = (g, x_in, out, cos, sin)
         cur.wait_stream(self.stream)
+        from . import _lib
+        self._device = dev.index if dev.index is not None else torch.cuda.current_device()
+        _lib.pin_workspace(self._device, True)
+        self._pinned = True
+
+    def close(self) -> None:
+        """Drops the graphs and unpins the workspace."""
+        if getattr(self, "_pinned", False):
+            from . import _lib
+            torch.cuda.synchronize(self._device)
+            self.graphs = {}
+            _lib.pin_workspace(self._device, False)
+            self._pinned = False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def _statics(self, t, dev):
         cos, sin = rope_constants(t)
@@ -170,6 +202,8 @@ class GraphedForward:
 
     def __call__(self, token_ids) -> torch.Tensor:
         ids = np.asarray(token_ids, np.int64)
+        if not getattr(self, "_pinned", False):
+            raise RuntimeError("GraphedForward is closed")
         g, x_in, out, _, _ = self.graphs[ids.size]
         x_in.copy_(torch.from_numpy(np.ascontiguousarray(self.model.embedding[ids], np.float32)))
         g.replay()

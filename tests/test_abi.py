@@ -89,7 +89,7 @@ GLU = _experts(8, 16)
 LIN = _experts(8, 16)
 
 
-@pytest.mark.parametrize("case", [
+MOE_UP_REJECTS = [
     dict(x=_input([3, 8], torch.float64), error=r"expected a 2D f32 or f16 tensor"),
     dict(glu=QuantExpertWeight(_input([16, 16]), GLU.scales, GLU.bias),
          error=r"w must be a quantW \[E·8, N\] weight"),
@@ -103,7 +103,10 @@ LIN = _experts(8, 16)
     dict(glu=QuantExpertWeight(GLU.w, GLU.scales, _input([16])), error=r"bias must be f32 \[2, 16\]"),
     dict(route=_input([3, 3]), error=r"route must be topk's f32 \[3, 8\] output"),
     dict(lin=_experts(8, 8), error=r"glu and lin weights must have the same shape"),
-])
+]
+
+
+@pytest.mark.parametrize("case", MOE_UP_REJECTS)
 def test_moe_up_rejects(case):
     # matmul.test.ts:311-371 (f16 activations are accepted here: an extension)
     x = case.get("x", X)
@@ -113,6 +116,43 @@ def test_moe_up_rejects(case):
     opts = {**MOE, **case.get("opts", {})}
     with pytest.raises(ValueError, match=case["error"]):
         rt.moeUp(x, route, glu, lin, opts)
+
+
+def _desc(v):
+    """moe_value_desc of a tensor or QuantW (ValueMeta: dtype, dims, elems)."""
+    if isinstance(v, QuantW):
+        dt, dims, elems = 2, list(v.dims), v.elems
+    else:
+        dt = {torch.float32: 0, torch.float16: 1}.get(v.dtype, 9)
+        dims, elems = list(v.shape), v.numel()
+    d = _lib.ValueDescC()
+    d.dtype, d.rank, d.elems = dt, len(dims), elems
+    for i, n in enumerate(dims[:4]):
+        d.dims[i] = n
+    return d
+
+
+@pytest.mark.parametrize("case", [c for c in MOE_UP_REJECTS
+                                  if "x" not in c and "same shape" not in c["error"]])
+def test_c_abi_check_expert_weight_messages(case):
+    """moe_check_expert_weight (the checkExpertWeight a native executor runs)
+    fails the same cases with the same messages as the host mirror, and
+    passes the valid weight with N and the expert count."""
+    lib = _lib.load()
+    route = case.get("route", ROUTE)
+    glu = case.get("glu", GLU)
+    opts = {**MOE, **case.get("opts", {})}
+    n, e = ctypes.c_int64(), ctypes.c_int64()
+    rc = lib.moe_check_expert_weight(b"moeUp", _desc(glu.w), _desc(glu.scales), _desc(glu.bias),
+                                     _desc(route), 8, 3, 4, opts["bits"], opts["groupSize"],
+                                     ctypes.byref(n), ctypes.byref(e))
+    assert rc == 1, case
+    msg = lib.moe_last_error().decode()
+    assert re.search(case["error"], msg), msg
+    assert msg.startswith("moeUp: ")
+    ok = lib.moe_check_expert_weight(b"moeUp", _desc(GLU.w), _desc(GLU.scales), _desc(GLU.bias),
+                                     _desc(ROUTE), 8, 3, 4, 8, 4, ctypes.byref(n), ctypes.byref(e))
+    assert ok == 0 and (n.value, e.value) == (16, 2)
 
 
 ACT = _input([12, 16])

@@ -1,8 +1,9 @@
 """The privacy-filter attention block (attnBlock.ts:28-57) on the GPU
 against an f64 composition of the pinned pieces (rmsNorm, dequantized
 Linears, oracle rope_f64 and sdpa_f64, + x), with int8 group-quantized qkv
-and out projections; and the model forward (model.ts:62-75) equal to its
-own chain of block calls, decoded by the Viterbi decoder."""
+and out projections; the whole model forward (model.ts:62-75) against an
+f64 composition of the pinned pieces, and equal to its own chain of block
+calls; graph replays equal to eager forwards."""
 import numpy as np
 import pytest
 import torch
@@ -64,18 +65,55 @@ def test_attention_block_against_f64(T):
     np.testing.assert_allclose(got.cpu().numpy(), want, atol=2e-4, rtol=1e-3)
 
 
-def moe_block(rng, E=8, k=4, I=640):
-    def expert(K, N):
+def moe_block(rng, E=8, k=4, I=640, with_ref=False):
+    refs = {}
+
+    def expert(name, K, N):
         q = rng.integers(-127, 128, size=(E, K, N)).astype(np.int8)
         sc = rng.uniform(0.5e-3, 2e-3, size=(E, N)).astype(np.float32)
         b = rng.standard_normal((E, N)).astype(np.float32) * 0.01
+        refs[name] = (q.astype(np.float64) * sc[:, None, :].astype(np.float64), b.astype(np.float64))
         words = pack_expert_weights(q, 8)
         d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
         return QuantExpertWeight(QuantW(d(words.view(np.int32)), (E * K, N)), d(sc), d(b))
-    return MoeBlock(norm_w=torch.from_numpy(rng.uniform(0.5, 1.5, 640).astype(np.float32)).to(DEV),
-                    router_w=torch.from_numpy(rng.standard_normal((640, E)).astype(np.float32) * 0.02).to(DEV),
-                    router_b=None, glu=expert(640, I), lin=expert(640, I), down=expert(I, 640),
-                    E=E, d=640, I=I, bits=8, group_up=640, group_down=I, k=k)
+    norm_w = rng.uniform(0.5, 1.5, 640).astype(np.float32)
+    router_w = rng.standard_normal((640, E)).astype(np.float32) * 0.02
+    blk = MoeBlock(norm_w=torch.from_numpy(norm_w).to(DEV), router_w=torch.from_numpy(router_w).to(DEV),
+                   router_b=None, glu=expert("glu", 640, I), lin=expert("lin", 640, I),
+                   down=expert("down", I, 640), E=E, d=640, I=I, bits=8, group_up=640,
+                   group_down=I, k=k)
+    if not with_ref:
+        return blk
+    refs.update(norm_w=norm_w.astype(np.float64), router_w=router_w.astype(np.float64), k=k)
+    return blk, refs
+
+
+_swiglu_f64 = np.vectorize(ref.swiglu, otypes=[np.float64])
+
+
+def moe_block_f64(x, r):
+    """EagerMoeMlp.forward (moeMlp.ts:79-121) in f64 from the pinned pieces:
+    rmsNorm, router = xn·W, topk (lowest id on ties, softmax over the picked
+    logits), dequantized expert products with the oracle's SwiGLU, + x.
+    Returns the output and the smallest gap between the k-th and (k+1)-th
+    logit over the tokens (the route is stable against rounding when it is
+    well above the f32 error of the logits)."""
+    k = r["k"]
+    xn = x / np.sqrt((x * x).mean(1, keepdims=True) + pf.RMS_EPS) * r["norm_w"]
+    logits = xn @ r["router_w"]
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    top = np.take_along_axis(logits, ids, 1)
+    gap = (top[:, k - 1] - np.sort(logits, axis=1)[:, -k - 1]).min()
+    gates = np.exp(top - top[:, :1])
+    gates /= gates.sum(1, keepdims=True)
+    out = x.copy()
+    (wg, bg), (wl, bl), (wd, bd) = r["glu"], r["lin"], r["down"]
+    for t in range(x.shape[0]):
+        for s in range(k):
+            e = ids[t, s]
+            act = _swiglu_f64(xn[t] @ wg[e] + bg[e], xn[t] @ wl[e] + bl[e])
+            out[t] += gates[t, s] * (act @ wd[e] + bd[e])
+    return out, gap
 
 
 def test_model_forward_is_its_block_chain_and_decodes():
@@ -110,6 +148,41 @@ def test_model_forward_is_its_block_chain_and_decodes():
     assert np.isfinite(hn).all()
 
 
+def test_model_forward_against_f64_composition():
+    """The whole 2-block network (model.ts:62-75: attention block, MoE
+    block, final rmsNorm, unembed) against an f64 composition of the pinned
+    pieces: attn_f64 (rope_f64, sdpa_f64, dequantized Linears) and the f64
+    MoE block. Logits within the layer bar, Viterbi labels equal."""
+    rng = np.random.default_rng(35)  # route gaps 1.7e-3 and 4.8e-3
+    blocks, refs = [], []
+    for _ in range(2):
+        attn, aref = make_attn(rng)
+        mlp, mref = moe_block(rng, with_ref=True)
+        blocks.append(pf.Block(attn, mlp))
+        refs.append((aref, mref))
+    unembed, uw, _ = qlinear(rng, 36, 640, 640, bias=False)
+    emb = rng.standard_normal((50, 640)).astype(np.float32)
+    model = pf.PrivacyFilterModel(emb, blocks, torch.ones(640, device=DEV), unembed)
+    T = 90
+    ids = rng.integers(0, 50, size=T)
+    say(f"model forward T={T} against f64")
+    got = model.forward(ids).cpu().numpy()
+    cos, sin = pf.rope_constants(T)
+    h = emb[ids].astype(np.float64)
+    for aref, mref in refs:
+        h = attn_f64(h, *aref, cos, sin)
+        h, gap = moe_block_f64(h, mref)
+        assert gap > 1e-3, f"route gap {gap}: pick another seed"
+    hn = h / np.sqrt((h * h).mean(1, keepdims=True) + pf.RMS_EPS)
+    want = hn @ uw.T
+    err = np.abs(got - want)
+    assert (err <= 2e-3 + 1e-2 * np.abs(want)).all(), f"max abs err {err.max()}"
+    info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
+    dec = pf.ViterbiDecoder(info)
+    assert dec.decode(pf.log_softmax_rows(got[:, :33])) == \
+        dec.decode(pf.log_softmax_rows(want[:, :33].astype(np.float32)))
+
+
 def test_graphed_forward_replays_equal_eager():
     # Replays with eager work and synchronisations between them, each against
     # the eager forward of the same ids (graph nodes must hold no memsets).
@@ -128,6 +201,15 @@ def test_graphed_forward_replays_equal_eager():
             want = model.forward(ids)
             torch.cuda.synchronize()
             assert torch.equal(got, want), (rep, t)
+    # the graphs pin the workspace: a longer text, which needs more, raises
+    # instead of moving it under them; after close() it runs
+    from runntime_amd.errors import RunntimeError
+    long_ids = rng.integers(0, 50, size=1500)
+    with pytest.raises(RunntimeError, match="pinned"):
+        model.forward(long_ids)
+    torch.cuda.synchronize()
+    gf.close()
+    assert torch.isfinite(model.forward(long_ids)).all()
 
 
 @pytest.mark.parametrize("T,K,N,bias,add", [(1, 640, 1152, True, False), (56, 896, 640, True, True),

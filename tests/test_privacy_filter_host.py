@@ -102,3 +102,32 @@ def test_native_viterbi_falls_back_to_argmax():
     dec.trans[:] = -np.inf
     lp = pf.log_softmax_rows(np.random.default_rng(9).standard_normal((6, 33)).astype(np.float32))
     assert dec.decode(lp) == ref.viterbi_decode(dec.start, dec.end, dec.trans, lp) == [int(j) for j in np.argmax(lp, 1)]
+
+
+def test_linear_and_attention_argument_checks():
+    """Shapes the kernels cannot check from raw pointers are refused on the
+    host, before any device call: a Linear's weight and bias, the rope
+    tables' rows (moe_attention reads T of them), the sinks."""
+    import torch
+    from runntime_amd.linear import Linear
+    w = torch.zeros((8, 4))
+    Linear(8, 4, w, torch.zeros(4))
+    with pytest.raises(ValueError, match="bias"):
+        Linear(8, 4, w, torch.zeros(5))
+    with pytest.raises(ValueError, match="bias"):
+        Linear(8, 4, w, torch.zeros(4, dtype=torch.float64))
+    with pytest.raises(ValueError, match="weight"):
+        Linear(8, 4, torch.zeros((4, 8)).t(), None)
+    lin_qkv = Linear(640, 1152, torch.zeros((640, 1152)))
+    lin_out = Linear(896, 640, torch.zeros((896, 640)))
+    blk = pf.AttnBlock(torch.ones(640), lin_qkv, lin_out, torch.zeros(14))
+    x = torch.zeros((10, 640))
+    cos, sin = (torch.from_numpy(a) for a in pf.rope_constants(10))
+    short = cos[:9].contiguous()
+    with pytest.raises(ValueError, match="cos"):
+        blk.forward(x, short, sin)
+    with pytest.raises(ValueError, match="sin"):
+        blk.forward(x, cos, sin.double())
+    bad = pf.AttnBlock(torch.ones(640), lin_qkv, lin_out, torch.zeros(13))
+    with pytest.raises(ValueError, match="sinks"):
+        bad.forward(x, cos, sin)
