@@ -48,6 +48,31 @@ def _compile(src: str) -> str:
     return obj
 
 
+NODE_INCLUDE = "/usr/include/node"
+NAPI_SRC = os.path.join(HERE, "napi", "runntime_moe_addon.cc")
+NAPI_OUT = os.path.join(HERE, "napi", "runntime_moe.node")
+
+
+def build_napi(verbose: bool = False):
+    """The Node addon (runntime_amd/napi/runntime_moe.node) over libmoe.so,
+    when Node's headers are installed; returns its path or None."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        if verbose:
+            print(f"no {NODE_INCLUDE}/node_api.h: the Node addon is not built")
+        return None
+    tmp = NAPI_OUT + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+           "-DNODE_GYP_MODULE_NAME=runntime_moe", f"-I{NODE_INCLUDE}", NAPI_SRC, f"-L{HERE}",
+           "-lmoe", "-Wl,-rpath,$ORIGIN/..", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"addon build failed:\n{r.stderr}")
+    os.replace(tmp, NAPI_OUT)
+    if verbose:
+        print(NAPI_OUT)
+    return NAPI_OUT
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
@@ -60,6 +85,7 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(LIB)
+    build_napi(verbose)
     return LIB
 
 
