@@ -201,15 +201,23 @@ def test_graphed_forward_replays_equal_eager():
             want = model.forward(ids)
             torch.cuda.synchronize()
             assert torch.equal(got, want), (rep, t)
-    # the graphs pin the workspace: a longer text, which needs more, raises
-    # instead of moving it under them; after close() it runs
+    # the graphs pin the workspace: a call that needs more than it holds
+    # (a layer whose act and partial products alone are 1.5 GB, more than any
+    # earlier test of this process grew it to) is refused before any launch
+    # instead of moving it under them; after close() the graphs are gone
+    import runntime_amd as rt
     from runntime_amd.errors import RunntimeError
-    long_ids = rng.integers(0, 50, size=1500)
+    from runntime_amd.synth import MoeConfig, make_inputs
+    big = MoeConfig("pin_T8192", 8192, 2048, 8, 8, 2048, "f16")
+    inp = make_inputs(big, seed=1)
     with pytest.raises(RunntimeError, match="pinned"):
-        model.forward(long_ids)
+        rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down, None, big.k)
     torch.cuda.synchronize()
     gf.close()
-    assert torch.isfinite(model.forward(long_ids)).all()
+    with pytest.raises(RuntimeError, match="closed"):
+        gf(rng.integers(0, 50, size=17))
+    ids = rng.integers(0, 50, size=40)
+    assert torch.isfinite(model.forward(ids)).all()
 
 
 @pytest.mark.parametrize("T,K,N,bias,add", [(1, 640, 1152, True, False), (56, 896, 640, True, True),
