@@ -181,6 +181,25 @@ MOE_API int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
               int k, int bits, int group_size_up, int group_size_down, float *route_out,
               float *out);
 
+/* moe_layer with no allocation: the same computation (bit for bit) on the
+ * same arguments, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid hipMalloc). No
+ * reference counterpart. The workspace is a static device array of
+ * MOE_NOALLOC_SCRATCH_BYTES per GPU, owned by the library until the process
+ * ends, instead of the context's growable one; the call allocates nothing
+ * and creates no timing events. A shape whose workspace exceeds it is
+ * INVALID_ARGUMENT with the size it needs (decode-sized calls fit: T·k of a
+ * few hundred rows). Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams or contexts without ordering)
+ * race. */
+#define MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+MOE_API int moe_layer_noalloc(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
+                              const float *w_router, const float *b_router,
+                              const moe_expert_weight *glu, const moe_expert_weight *lin,
+                              const moe_expert_weight *down, const float *residual, int T, int d,
+                              int I, int E, int k, int bits, int group_size_up,
+                              int group_size_down, float *route_out, float *out);
+
 /* EagerMoeMlp.forward for the quantized formats
  * (src/zoo/privacy-filter/moeMlp.ts:79-121): xn = rmsNorm(x, norm_w, eps),
  * route = topk(xn·W + b, k), out = x + moeDown(moeUp(xn, route, glu, lin),

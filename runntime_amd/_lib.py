@@ -15,6 +15,8 @@ MOE_F32 = 0
 MOE_F16 = 1
 # MOE_NULL_STREAM: the null (legacy default) stream as a stream argument.
 MOE_NULL_STREAM = 1
+# include/runntime_moe.h MOE_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/runntime_moe.h declares.
 EXPORTED = (
@@ -26,7 +28,7 @@ EXPORTED = (
     "moe_block", "moe_rmsnorm", "moe_matmul_gather", "moe_block_float", "moe_rope",
     "moe_sdpa", "moe_linear", "moe_viterbi_decode", "moe_attention", "moe_ctx_pin_workspace",
     "moe_check_expert_weight", "moe_buffer_alloc", "moe_buffer_free", "moe_buffer_write",
-    "moe_buffer_read",
+    "moe_buffer_read", "moe_layer_noalloc",
 )
 PROF_GROUPS = ("topk", "router", "dispatch", "up", "down", "combine", "norm")
 
@@ -80,6 +82,7 @@ def load() -> ctypes.CDLL:
             "moe_up": ([P, P, I, P, W, W, I, I, I, I, I, I, I, P], I),
             "moe_down": ([P, P, P, W, P, I, I, I, I, I, I, I, P], I),
             "moe_layer": ([P, P, I, P, P, W, W, W, P, I, I, I, I, I, I, I, I, P, P], I),
+            "moe_layer_noalloc": ([P, P, I, P, P, W, W, W, P, I, I, I, I, I, I, I, I, P, P], I),
             "moe_dispatch": ([P, P, I, I, I, P, P], I),
             "moe_pack_quantw": ([P, P, I, I, I, I, P], I),
             "moe_prof_enable": ([P, I], I),

@@ -224,13 +224,16 @@ def moeDown(act, route, out: QuantExpertWeight, residual, opts) -> torch.Tensor:
 def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWeight,
               down: QuantExpertWeight, residual, k: int, bits: int = 8,
               group_size_up=None, group_size_down=None, return_route: bool = False,
-              out=None, route=None):
+              out=None, route=None, noalloc: bool = False):
     """The routed layer in one call (EagerMoeMlp.forward's quantized branch
     after the norm, zoo/privacy-filter/moeMlp.ts:82-121):
     route = topk(x·Wr + br, k); act = moeUp(x, route, glu, lin);
     out = moeDown(act, route, down, residual). Group sizes default to one
     scale per output channel (K of each projection). `out` (f32 [T, d]) and
-    `route` (f32 [T, 2k]) may be given to write into existing buffers."""
+    `route` (f32 [T, 2k]) may be given to write into existing buffers.
+    noalloc: run moe_layer_noalloc, whose workspace is the library's static
+    per-GPU scratch (no device allocation by the call; give `out` and
+    `route` to allocate nothing here either)."""
     t, d, _ = _want2d("moe_layer", x, ("f32", "f16"))
     rw = _dims(router_w)
     if _dtype_name(router_w) != "f32" or len(rw) != 2 or rw[0] != d:
@@ -258,10 +261,10 @@ def moe_layer(x, router_w, router_b, glu: QuantExpertWeight, lin: QuantExpertWei
         raise ValueError(f"moe_layer: out must be contiguous f32 [{t}, {d}]")
     g, l_, dn = _weight_c(glu), _weight_c(lin), _weight_c(down)
     lib = _lib.load()
-    _lib.check(lib.moe_layer(_ctx(dev), x.data_ptr(), _xdtype(x), router_w.data_ptr(),
-                             _ptr(router_b), ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn),
-                             _ptr(residual), t, d, i, e, k, bits, gu, gd, route.data_ptr(),
-                             out.data_ptr()))
+    fn = lib.moe_layer_noalloc if noalloc else lib.moe_layer
+    _lib.check(fn(_ctx(dev), x.data_ptr(), _xdtype(x), router_w.data_ptr(), _ptr(router_b),
+                  ctypes.byref(g), ctypes.byref(l_), ctypes.byref(dn), _ptr(residual), t, d, i, e,
+                  k, bits, gu, gd, route.data_ptr(), out.data_ptr()))
     return (out, route) if return_route else out
 
 

@@ -7,6 +7,8 @@
 
 #include "moe_internal.h"
 
+#include <mutex>
+
 // ------------------------------------------------------------------ errors
 
 static thread_local std::string g_last_error;
@@ -37,14 +39,14 @@ static hipEvent_t prof_event(moe_ctx *c) {
   return e;
 }
 
-ProfScope::ProfScope(moe_ctx *c, int g) : ctx(c), group(g) {
-  if (!ctx->prof_on) return;
+ProfScope::ProfScope(moe_ctx *c, int g, bool enable) : ctx(c), group(g), on(enable && c->prof_on) {
+  if (!on) return;
   b = prof_event(ctx);
   if (b) (void)hipEventRecord(b, ctx->stream);
 }
 
 ProfScope::~ProfScope() {
-  if (!ctx->prof_on || !b) return;
+  if (!on || !b) return;
   hipEvent_t e = prof_event(ctx);
   if (!e) return;
   (void)hipEventRecord(e, ctx->stream);
@@ -83,6 +85,37 @@ extern "C" int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *c
 
 // ------------------------------------------------------------------ context
 
+// ------------------------------------------------ allocation-free scratch
+//
+// moe_layer_noalloc's workspace: a file-scope device array, one per GPU the
+// library runs on, held until the process ends. Host code never uses the
+// array's name as an address (on the host it is a stand-in, not device
+// memory): its address on each device comes from hipGetSymbolAddress, taken
+// once per device with that device current (at moe_ctx_create), and only
+// that pointer goes to kernels.
+static __device__ __align__(256) char scratch[MOE_NOALLOC_SCRATCH_BYTES];
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static char *g_scratch_ptr[SCRATCH_MAX_DEVICES];
+static hipError_t g_scratch_err[SCRATCH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// The scratch address on `device` (current); NULL and an error if unknown.
+static char *scratch_on(int device, hipError_t *err) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0 || device >= SCRATCH_MAX_DEVICES) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  if (!g_scratch_ptr[device] && g_scratch_err[device] == hipSuccess) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) g_scratch_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+    else g_scratch_ptr[device] = (char *)p;
+  }
+  *err = g_scratch_err[device];
+  return g_scratch_ptr[device];
+}
+
 extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
   if (!out) return moe_fail(MOE_INVALID_ARGUMENT, "moe_ctx_create: out is NULL");
   int n = 0;
@@ -92,6 +125,10 @@ extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
     return moe_fail(MOE_INVALID_ARGUMENT, "moe_ctx_create: device " + std::to_string(device) +
                                               " out of range (" + std::to_string(n) + " visible)");
   MOE_HIP_CHECK(hipSetDevice(device));
+  // The allocation-free entry point's scratch on this device (once per
+  // device; its failure surfaces only in moe_layer_noalloc).
+  hipError_t scratch_err = hipSuccess;
+  (void)scratch_on(device, &scratch_err);
   moe_ctx *c = new moe_ctx();
   c->device = device;
   if (stream == MOE_NULL_STREAM) {
@@ -249,9 +286,17 @@ struct LayerWs {
 
 // Workspace for `calls` calls over T tokens each (A = T·k assignments per
 // call). Sections that a call does not need have size 0.
+// A workspace given instead of the context's (the allocation-free entry
+// point): base and size; base NULL means the context workspace.
+struct FixedWs {
+  char *base = nullptr;
+  size_t size = 0;
+  const char *op = "";
+};
+
 static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_floats,
                    size_t partial_floats, size_t act_floats, size_t y_floats, LayerWs &L,
-                   size_t xn_bytes = 0) {
+                   size_t xn_bytes = 0, const FixedWs *fixed = nullptr) {
   const int A = T * k;
   const int nblk = (A + DISPATCH_TILE - 1) / DISPATCH_TILE;
   const size_t C = (size_t)calls;
@@ -268,9 +313,19 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   size_t o_actv = p.take(sizeof(float) * C * act_floats);
   size_t o_y = p.take(sizeof(float) * C * y_floats);
   size_t o_xn = p.take(C * xn_bytes);
-  int rc = moe_ws_ensure(ctx, p.off);
-  if (rc) return rc;
-  char *b = ctx->ws;
+  char *b = nullptr;
+  if (fixed && fixed->base) {
+    if (p.off > fixed->size)
+      return moe_fail(MOE_INVALID_ARGUMENT,
+                      std::string(fixed->op) + ": needs " + std::to_string(p.off) +
+                          " bytes of workspace; the static scratch holds " +
+                          std::to_string(fixed->size));
+    b = fixed->base;
+  } else {
+    int rc = moe_ws_ensure(ctx, p.off);
+    if (rc) return rc;
+    b = ctx->ws;
+  }
   L.db.blk_counts = (int32_t *)(b + o_cnt);
   L.db.blk_base = (int32_t *)(b + o_base);
   L.db.offsets = (int32_t *)(b + o_off);
@@ -476,8 +531,9 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
                       const moe_expert_weight *lin, const moe_expert_weight *down,
                       const void *residual, moe_dtype res_dtype, int T, int d, int I, int E,
                       int k, int bits, int group_size_up, int group_size_down, float *route_out,
-                      float *out) {
+                      float *out, const FixedWs *fixed = nullptr) {
   const std::string o(op);
+  const bool timing = !(fixed && fixed->base);
   int rc = check_ctx(ctx, op);
   if (rc) return rc;
   if ((rc = check_k(op, k, E, true))) return rc;
@@ -552,12 +608,12 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   const size_t esize = x_dtype == MOE_F16 ? 2 : 4;
   if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
                     router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L,
-                    norm ? (size_t)T * d * esize : 0)))
+                    norm ? (size_t)T * d * esize : 0, fixed)))
     return rc;
   hipStream_t s = ctx->stream;
   if (norm) {
     // The router and the gate/up product read xn; the residual stays x.
-    ProfScope ps(ctx, PG_NORM);
+    ProfScope ps(ctx, PG_NORM, timing);
     NormArgs na{x, norm->weight, nullptr, L.xn, x_dtype, T, d, d, d, norm->eps, 1.0f};
     if ((rc = launch_rmsnorm(na, s))) return rc;
     x = L.xn;
@@ -572,25 +628,25 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   dn.out = L.y;
   bool dispatched = false;
   {
-    ProfScope ps(ctx, PG_ROUTER);
+    ProfScope ps(ctx, PG_ROUTER, timing);
     RouterArgs ra{x, x_dtype, st->x, w_router, st->router_w, b_router, st->router_b, route,
                   route_cs, L.partial, T, d, E, k, calls};
     if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
   }
   if (!dispatched) {
-    ProfScope ps(ctx, PG_DISPATCH);
+    ProfScope ps(ctx, PG_DISPATCH, timing);
     if ((rc = launch_dispatch(route, route_cs, T, E, k, calls, TILE_M, L.db, s))) return rc;
   }
   {
-    ProfScope ps(ctx, PG_UP);
+    ProfScope ps(ctx, PG_UP, timing);
     if ((rc = launch_expert(up, L.db, s))) return rc;
   }
   {
-    ProfScope ps(ctx, PG_DOWN);
+    ProfScope ps(ctx, PG_DOWN, timing);
     if ((rc = launch_expert(dn, L.db, s))) return rc;
   }
   {
-    ProfScope ps(ctx, PG_COMBINE);
+    ProfScope ps(ctx, PG_COMBINE, timing);
     if ((rc = launch_combine(L.y, dn.out_cs, dn.parts, (int64_t)A * d, route, route_cs, residual,
                              res_dtype, st->residual, T, d, E, k, out, st->out, calls, s)))
       return rc;
@@ -608,6 +664,29 @@ extern "C" int moe_layer_batched(moe_ctx *ctx, int calls, const moe_call_strides
   return layer_impl("moe_layer", ctx, calls, st, x, x_dtype, nullptr, w_router, b_router, glu,
                     lin, down, residual, MOE_F32, T, d, I, E, k, bits, group_size_up,
                     group_size_down, route_out, out);
+}
+
+extern "C" int moe_layer_noalloc(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
+                                 const float *w_router, const float *b_router,
+                                 const moe_expert_weight *glu, const moe_expert_weight *lin,
+                                 const moe_expert_weight *down, const float *residual, int T,
+                                 int d, int I, int E, int k, int bits, int group_size_up,
+                                 int group_size_down, float *route_out, float *out) {
+  int rc = check_ctx(ctx, "moe_layer_noalloc");
+  if (rc) return rc;
+  hipError_t e = hipSuccess;
+  char *base = scratch_on(ctx->device, &e);
+  if (!base)
+    return moe_fail(MOE_EXECUTION_FAILED, std::string("moe_layer_noalloc: no scratch address on "
+                                                      "device ") + std::to_string(ctx->device) +
+                                              ": " + hipGetErrorString(e));
+  FixedWs fixed;
+  fixed.base = base;
+  fixed.size = MOE_NOALLOC_SCRATCH_BYTES;
+  fixed.op = "moe_layer_noalloc";
+  return layer_impl("moe_layer_noalloc", ctx, 1, nullptr, x, x_dtype, nullptr, w_router, b_router,
+                    glu, lin, down, residual, MOE_F32, T, d, I, E, k, bits, group_size_up,
+                    group_size_down, route_out, out, &fixed);
 }
 
 extern "C" int moe_block(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const void *norm_w,

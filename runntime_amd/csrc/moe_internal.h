@@ -58,8 +58,10 @@ extern const char *const PROF_NAMES[PROF_GROUPS];
 struct ProfScope {
   moe_ctx *ctx;
   int group;
+  bool on;
   hipEvent_t b = nullptr;
-  ProfScope(moe_ctx *c, int g);
+  // enable false: no timing (the allocation-free entry point creates no events)
+  ProfScope(moe_ctx *c, int g, bool enable = true);
   ~ProfScope();
 };
 
