@@ -16,7 +16,8 @@
 // from two sources of 64 units each: up takes the same 64 units (256
 // outputs) of glu and of lin, down takes 128 consecutive units of its one
 // weight (512 outputs). Two wavefront shapes:
-//  - f16 A (up with f16 x): each wavefront takes all 128 rows and 16 slots
+//  - f16 A (up with f16 x when gemm_wide.hip does not take the shape): each
+//    wavefront takes all 128 rows and 16 slots
 //    (8 glu units and the same 8 lin units) with two of each unit's four
 //    columns per lane: 4 × 2 v_mfma_f32_32x32x16_f16 tiles, so one
 //    converted weight fragment feeds four MFMAs. The SwiGLU pairs lanes 16
@@ -70,7 +71,7 @@
 namespace {
 
 // OPAIR (up): write act as f16 pairs. AT = f16pair (down): read them.
-template <int MODE, typename AT, bool OPAIR, bool PAIR, int DBG = 0>
+template <int MODE, typename AT, bool OPAIR, bool PAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_expert_gemm(GemmArgs p) {
   constexpr bool SPLIT = sizeof(AT) == 4;
@@ -250,7 +251,6 @@ void k_expert_gemm(GemmArgs p) {
   };
   // Load instruction q of step ks into slot `stage`: q < 2 weights, else A.
   auto issue_q = [&](const Params &P, int ks, int stage, int q) {
-    if ((DBG & 1) && q < 2) return;
     const uint32_t st = lds0 + stage * STAGE;
     if (q < 2) dma16(P.wr, P.woff[q], ks * (TPS * 16), st + (2 * wave + q) * 1024);
     else dma16(ar, P.aoff[q - 2], ks * BK * (int)sizeof(AT), st + W_BYTES + (AI * wave + q - 2) * 1024);
@@ -288,13 +288,8 @@ void k_expert_gemm(GemmArgs p) {
   auto read_frags = [&](Frags &F, int stage, int kk) {
     const uint8_t *st = lds + stage * STAGE;
     const int t0 = 4 * h + 2 * kk;
-    if constexpr ((DBG & 2) != 0) {
-      F.w[kk][0] = WV{} + (uint32_t)lane;
-      F.w[kk][1] = WV{} + (uint32_t)stage;
-    } else {
     F.w[kk][0] = *(const WV *)(st + boff + ((t0 ^ bsw) * 16) + wdw);
     F.w[kk][1] = *(const WV *)(st + boff + (((t0 + 1) ^ bsw) * 16) + wdw);
-    }
 #pragma unroll
     for (int i = 0; i < RT; i++) {
       if constexpr (SPLIT) {
@@ -735,13 +730,10 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   // Paired steps (one barrier per 64 k) when each part has an even number
   // of steps.
   const bool pair = p.kpart % 2 == 0;
-  if (gemm_wide_eligible(ea) && !getenv("MOE_DEV_NARROW")) return launch_gemm_up_wide(p, (int)blocks, pairs, s);
+  // Up with f16 x: weights straight into registers (gemm_wide.hip).
+  if (gemm_wide_eligible(ea)) return launch_gemm_up_wide(p, (int)blocks, pairs, s);
 #define LAUNCH_P(M_, AT_, OP_)                                                            \
   do {                                                                                    \
-    if (pair && M_ == MODE_UP && getenv("MOE_DEV_NDBG")) { const int d_ = atoi(getenv("MOE_DEV_NDBG")); \
-      if (d_ == 1) hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true, 1>), grid, block, 0, s, p); \
-      else if (d_ == 2) hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true, 2>), grid, block, 0, s, p); \
-      else hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true, 3>), grid, block, 0, s, p); } else \
     if (pair) hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true>), grid, block, 0, s, p); \
     else hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, false>), grid, block, 0, s, p);  \
   } while (0)

@@ -28,13 +28,17 @@
 // buffers. Measured on config 4's up shape: weights through LDS (a
 // direct-to-LDS load and a read per byte) took about a third of the
 // kernel's time; 8-byte loads straight into registers kept the texture
-// data path 88% busy; 16-byte loads halve its instructions.
+// data path 88% busy; 16-byte loads halve its instructions. Loads that
+// each cover whole lines (one source per instruction) need a DPP exchange
+// and selects per step and measured 7% slower.
 //
 // x rows (shared by all eight wavefronts) come through LDS by direct buffer
-// loads (buffer_load … lds) into a ring of SA steps, gathered through the
-// dispatch permutation; one workgroup barrier per step. x's k order inside
-// a step follows the weights': slice kk of lane half h reads 16-byte chunk
-// 2h + kk of the row's 64 bytes.
+// loads (buffer_load … lds), gathered through the dispatch permutation, in
+// step pairs: 64 k of a row is 128 bytes, one whole cache line (one step's
+// 64 bytes per row took 12-17% longer over the kernel, with a barrier per
+// step); one workgroup barrier per pair. x's k order inside a step follows
+// the weights': slice kk of lane half h reads 16-byte chunk 4q + 2h + kk of
+// the pair's row (q: the step's place in the pair).
 //
 // Waits: the weight loads are ordinary loads whose waits the compiler places
 // (it counts only its own loads, so it waits a little longer than needed).
@@ -64,7 +68,7 @@ constexpr int WD_BASE_WAIT = WD_WLOADS + WD_WLOADS * (2 * WD_SP - 3) + WD_ALOADS
 static_assert(WD_BASE_WAIT + WD_TILE_LOADS < 64, "vmcnt range");
 constexpr int wd_wait(int n) { return n < 63 ? n : 63; }
 
-template <bool OPAIR, int DBG>
+template <bool OPAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gemm_up_direct(GemmArgs p) {
   __shared__ __align__(16) uint8_t aring[WD_SP * WD_P_STAGE];
@@ -190,14 +194,7 @@ void k_gemm_up_direct(GemmArgs p) {
   };
 
   u32x4 wr[WD_NB][2];  // two whole quantW tiles per step, four steps
-  if constexpr (DBG & 1) {
-#pragma unroll
-    for (int b = 0; b < WD_NB; b++)
-#pragma unroll
-      for (int t = 0; t < 2; t++) wr[b][t] = u32x4{(uint32_t)lane * 0x01010101u, 3u * t + 5u * b, 7u, 9u};
-  }
   auto load_w = [&](u32x4 (&dst)[2], const uint8_t *base, int ks) {
-    if constexpr (DBG & 1) return;
     const uint8_t *q = base + (uint32_t)ks * (BK * 4);
 #pragma unroll
     for (int t = 0; t < 2; t++) dst[t] = *(const u32x4 *)(q + 16 * t);
@@ -237,12 +234,6 @@ void k_gemm_up_direct(GemmArgs p) {
     for (int i = 0; i < WD_RT; i++) F[i] = *(const u32x4 *)(st + arow[i] + ((c ^ asw[i]) * 16));
   };
   auto mfma_slice = [&](const u32x4 (&F)[WD_RT], const StepB &w, int kk) {
-    if constexpr (DBG & 2) {
-#pragma unroll
-      for (int i = 0; i < WD_RT; i++)
-        acc[i][kk][0] += __builtin_bit_cast(float, F[i][0] ^ w.b[kk][0][0] ^ w.b[kk][1][1]);
-      return;
-    }
     half8 bf[WD_CT];
     bf[0] = cvt_i8x8(w.b[kk][0][0], w.b[kk][0][1]);
 #pragma unroll
@@ -449,11 +440,7 @@ bool gemm_wide_eligible(const ExpertArgs &ea) {
 
 int launch_gemm_up_wide(const GemmArgs &p, int blocks, bool pairs, hipStream_t s) {
   dim3 grid((unsigned)blocks), block(WD_WAVES * WAVE);
-  const char *dv = getenv("MOE_DEV_WIDE_DBG");
-  const int dbg = dv ? atoi(dv) : 0;
-#define WL(D) do { if (pairs) hipLaunchKernelGGL((k_gemm_up_direct<true, D>), grid, block, 0, s, p); \
-  else hipLaunchKernelGGL((k_gemm_up_direct<false, D>), grid, block, 0, s, p); } while (0)
-  if (dbg == 1) WL(1); else if (dbg == 2) WL(2); else if (dbg == 3) WL(3); else WL(0);
-#undef WL
+  if (pairs) hipLaunchKernelGGL((k_gemm_up_direct<true>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_gemm_up_direct<false>), grid, block, 0, s, p);
   return 0;
 }
