@@ -64,8 +64,24 @@ def layer_flops(cfg):
 TRAFFIC_PROFILES = {2: "k_expert_skinny_up_c2_decode_traffic.md",
                     3: "k_expert_skinny_up_c3_batched_decode_traffic.md",
                     "3-sequential": "k_expert_skinny_up_c3_decode_traffic.md",
-                    4: "k_expert_gemm_c4_prefill_traffic.md",
-                    5: "k_expert_gemm_c5_prefill_traffic.md"}
+                    4: "k_gemm_up_direct_c4_prefill_traffic.md",
+                    5: "k_gemm_up_direct_c5_prefill_traffic.md"}
+
+
+def source_sha():
+    """SHA-256 (first 12 hex digits) over the kernel sources, runntime_amd/csrc/
+    *.hip, *.h and *.cpp in name order: the same hash heads every kernel
+    profile under profiles/, so a bench line and a profile of the same kernels
+    can be matched."""
+    import hashlib
+    csrc = os.path.join(ROOT, "runntime_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:12]
 
 
 def profiled_traffic(config, default_shape):
@@ -533,7 +549,7 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                     "traffic": traffic, "traffic_source": traffic_src,
-                    "kernel": "gate/up grouped GEMM",
+                    "kernel": "k_gemm_up_direct (gate/up grouped GEMM + SwiGLU)",
                     "algorithmic_flops_per_launch": fl, "avg_launch_us": round(up_avg_s * 1e6, 2)}
         layer_frac = layer_flops(cfg) * calls / (ms_per_step / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS
 
@@ -555,6 +571,7 @@ def main():
         "layer_roofline_frac": round(layer_frac, 4),
         "kernel_ms": {g: round(ms / n, 5) for g, (ms, n) in groups.items()},
         "roofline": roofline,
+        "source_sha": source_sha(),
     }
     if args.config == 2 and not args.no_sequential:
         say("sequential (launch-bound) rate")
