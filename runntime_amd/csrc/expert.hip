@@ -26,6 +26,7 @@
 #include <stdlib.h>
 
 #include "moe_internal.h"
+#include "norm_dev.h"
 
 namespace {
 
@@ -54,6 +55,8 @@ struct ExpertKArgs {
   int64_t out_cs;
   int rc;  // rows staged per chunk (skinny kernel)
   DispatchBufs db;
+  const float *a_inv;   // moe_block's pre-norm (up, skinny kernel), or NULL
+  const void *a_normw;
 };
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
@@ -300,6 +303,18 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
             AT e[EPC];
 #pragma unroll
             for (int j = 0; j < EPC; j++) e[j] = (ok && k + j < p.K) ? xr[k + j] : (AT)0;
+            v[u] = __builtin_bit_cast(u32x4, e);
+          }
+          if (p.a_normw) {
+            // moe_block's pre-norm while staging: x·inv·w in f32, rounded
+            // to x's dtype, as the standalone norm stores it.
+            const AT *nw = (const AT *)p.a_normw;
+            const float inv = ok ? p.a_inv[src] : 0.f;
+            AT e[EPC];
+            __builtin_memcpy(e, &v[u], sizeof(e));
+#pragma unroll
+            for (int j = 0; j < EPC; j++)
+              if (ok && k + j < p.K) e[j] = (AT)moe_dev::norm_value<AT>((float)e[j], inv, (float)nw[k + j]);
             v[u] = __builtin_bit_cast(u32x4, e);
           }
         }
@@ -719,7 +734,14 @@ bool expert_uses_gemm(const ExpertArgs &ea) {
   return ea.calls == 1 && want_gemm && gemm_eligible(ea);
 }
 
+bool expert_stages_norm(const ExpertArgs &ea) {
+  return ea.mode == MODE_UP && !expert_uses_gemm(ea) && ea.bits == 8 &&
+         (ea.g == ea.K || ea.g % 32 == 0);
+}
+
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
+  if (ea.a_normw && (!expert_stages_norm(ea) || !ea.a_inv))
+    return moe_fail(MOE_EXECUTION_FAILED, "expert: the staged pre-norm needs the skinny gate/up kernel");
   MOE_NONNULL(ea.a);
   MOE_NONNULL(ea.route);
   MOE_NONNULL(ea.w0.w);
@@ -757,6 +779,8 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   p.w1_cs = ea.w1_cs;
   p.s1_cs = ea.s1_cs;
   p.b1_cs = ea.b1_cs;
+  p.a_inv = ea.a_inv;
+  p.a_normw = ea.a_normw;
   p.K = ea.K;
   p.N = ea.N;
   p.E = ea.E;

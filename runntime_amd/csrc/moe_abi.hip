@@ -606,12 +606,20 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
 
   LayerWs L;
   const size_t esize = x_dtype == MOE_F16 ? 2 : 4;
+  // The pre-norm: folded into the router's and the skinny gate/up kernel's
+  // staging (the router's chunk kernel leaves each token's inverse RMS in
+  // the xn slot), or, for the grouped GEMM (loads straight into LDS), a
+  // normalised copy xn.
+  const bool stage_norm = norm && expert_stages_norm(up);
   if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
                     router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L,
-                    norm ? (size_t)T * d * esize : 0, fixed)))
+                    norm ? (stage_norm ? (size_t)T * 4 : (size_t)T * d * esize) : 0, fixed)))
     return rc;
   hipStream_t s = ctx->stream;
-  if (norm) {
+  if (stage_norm) {
+    up.a_inv = (const float *)L.xn;
+    up.a_normw = norm->weight;
+  } else if (norm) {
     // The router and the gate/up product read xn; the residual stays x.
     ProfScope ps(ctx, PG_NORM, timing);
     NormArgs na{x, norm->weight, nullptr, L.xn, x_dtype, T, d, d, d, norm->eps, 1.0f};
@@ -630,7 +638,9 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   {
     ProfScope ps(ctx, PG_ROUTER, timing);
     RouterArgs ra{x, x_dtype, st->x, w_router, st->router_w, b_router, st->router_b, route,
-                  route_cs, L.partial, T, d, E, k, calls};
+                  route_cs, L.partial, T, d, E, k, calls,
+                  stage_norm ? norm->weight : nullptr, norm ? norm->eps : 0.f,
+                  stage_norm ? (float *)L.xn : nullptr};
     if ((rc = launch_router_topk(ra, &L.db, TILE_M, &dispatched, s))) return rc;
   }
   if (!dispatched) {

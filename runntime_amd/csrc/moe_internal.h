@@ -148,6 +148,12 @@ struct RouterArgs {
   int64_t route_cs;
   float *partial;  // workspace, T·J·E floats per call
   int T, d, E, k, calls;
+  // moe_block's pre-norm, applied while staging x (one call): weight [d] of
+  // x's dtype, or NULL; the chunk kernels also write each token's inverse
+  // RMS to inv [T].
+  const void *norm_w;
+  float norm_eps;
+  float *inv;
 };
 // Router + top-k. With T <= FUSED_T and `db` given, the dispatch of each call
 // is built in the same kernel and `dispatched` is set.
@@ -185,6 +191,11 @@ struct ExpertArgs {
   // Down on the grouped GEMM: K split into `parts` halves whose partial
   // products go to out + part·A·N (the combine adds them). 0 or 1 = whole K.
   int parts;
+  // Up of moe_block on the skinny kernel: x is normalised while staging,
+  // row t scaled by a_inv[t] (written by the router) and the weight
+  // a_normw [K] of x's dtype; NULL for plain x.
+  const float *a_inv;
+  const void *a_normw;
 };
 
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
@@ -192,6 +203,9 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 bool gemm_eligible(const ExpertArgs &ea);
 // Whether launch_expert runs these arguments on the grouped GEMM.
 bool expert_uses_gemm(const ExpertArgs &ea);
+// Whether the gate/up product can normalise x while staging it (a_inv,
+// a_normw): the skinny MFMA kernel.
+bool expert_stages_norm(const ExpertArgs &ea);
 // K parts the grouped GEMM uses for this down product (1 or 2): 2 when the
 // split evens out the last round of tiles over the CUs.
 int gemm_down_parts(const ExpertArgs &ea);

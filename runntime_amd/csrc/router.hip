@@ -17,6 +17,7 @@
 // wavefront: a logit is a candidate only if it is strictly above the
 // reference's −3.4e38 start value (so NaN never enters), and a slot no
 // candidate fills keeps (−3.4e38, id 0), as the reference's does.
+#include "norm_dev.h"
 #include "router_dev.h"
 
 namespace {
@@ -69,6 +70,23 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   const int et = min(RT_EXPERTS, E - e0);
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
+  // moe_block's pre-norm: each wavefront takes the inverse RMS of four of
+  // the tile's tokens (the canonical order); the first chunk's blocks store it.
+  __shared__ float sinv[RT_TOKENS];
+  const T *nw = (const T *)ra.norm_w;
+  if (nw) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    for (int tt = threadIdx.x / WAVE; tt < RT_TOKENS; tt += 256 / WAVE) {
+      const int t = t0 + tt;
+      if (t >= Tn) break;
+      const float inv = moe_dev::wave_row_inv(x + (int64_t)t * d, d, ra.norm_eps, lane);
+      if (lane == 0) {
+        sinv[tt] = inv;
+        if (j == 0 && blockIdx.z % etiles == 0) ra.inv[t] = inv;
+      }
+    }
+    __syncthreads();
+  }
   // Staging: every load of the tile is issued before the first LDS store.
   constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
   float xv[XPER], wv[WPER];
@@ -78,6 +96,8 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
     int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
     int t = t0 + tt;
     xv[r] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+    if (nw && t < Tn && kk < len)
+      xv[r] = moe_dev::norm_value<T>(xv[r], sinv[tt], load_as_f32(nw, k0 + kk));
   }
 #pragma unroll
   for (int r = 0; r < WPER; r++) {
@@ -279,6 +299,22 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
   const int tid = threadIdx.x;
+  // moe_block's pre-norm (as k_router_chunks): the tile's inverse RMS values.
+  __shared__ float sinv[TB];
+  const T *nw = (const T *)ra.norm_w;
+  if (nw) {
+    const int lane = tid & (WAVE - 1);
+    for (int tt = tid / WAVE; tt < TB; tt += 256 / WAVE) {
+      const int t = t0 + tt;
+      if (t >= Tn) break;
+      const float inv = moe_dev::wave_row_inv(x + (int64_t)t * d, d, ra.norm_eps, lane);
+      if (lane == 0) {
+        sinv[tt] = inv;
+        if (j == 0 && blockIdx.z % etiles == 0) ra.inv[t] = inv;
+      }
+    }
+    __syncthreads();
+  }
   // Staging in 16-byte loads where the chunk is whole and aligned: x as
   // 8-element runs of a token's row (stored transposed), W as 4-expert runs.
   const bool vec = len == ROUTER_CHUNK && (d & 7) == 0 && (E & 3) == 0 && e0 + EB <= E;
@@ -302,6 +338,10 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
 #pragma unroll
         for (int q = 0; q < 8; q++) v[q] = 0.f;
       }
+      if (nw && t < Tn) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = moe_dev::norm_value<T>(v[q], sinv[tt], load_as_f32(nw, k0 + kk + q));
+      }
 #pragma unroll
       for (int q = 0; q < 8; q++) xs[(kk + q) * TB + tt] = v[q];
     }
@@ -312,7 +352,9 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   } else {
     for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
       const int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK, t = t0 + tt;
-      xs[kk * TB + tt] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+      float v = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
+      if (nw && t < Tn && kk < len) v = moe_dev::norm_value<T>(v, sinv[tt], load_as_f32(nw, k0 + kk));
+      xs[kk * TB + tt] = v;
     }
     for (int i = tid; i < ROUTER_CHUNK * EB; i += 256) {
       const int kk = i / EB, ee = i % EB, e = e0 + ee;

@@ -119,11 +119,21 @@ def test_moe_block_matches_oracle(cid, sample):
     assert_close(got_out[tokens], want_out, what=f"block config {cid}")
 
 
-@pytest.mark.parametrize("cid", [1, 3])
-def test_moe_block_is_norm_then_layer(cid):
-    """moe_block = rmsNorm → moe_layer(xn) with residual x, bit for bit."""
+@pytest.mark.parametrize("cid,T,x_dtype", [(1, None, None), (3, None, None), (2, 100, None),
+                                           (2, 100, "f16"), (2, 40, "f16"), (4, None, None)])
+def test_moe_block_is_norm_then_layer(cid, T, x_dtype):
+    """moe_block = rmsNorm → moe_layer(xn) with residual x, bit for bit.
+    The block normalises x while staging it where the gate/up product runs on
+    the skinny kernel (configs 1-3 and the T = 40 / 100 cases: the fused and
+    the register-tiled router) and through a normalised copy for the grouped
+    GEMM (config 4)."""
+    import dataclasses
     cfg = CONFIGS[cid]
-    say(f"moe_block composition config {cid}")
+    if T:
+        cfg = dataclasses.replace(cfg, T=T)
+    if x_dtype:
+        cfg = dataclasses.replace(cfg, x_dtype=x_dtype)
+    say(f"moe_block composition config {cid} T={cfg.T} {cfg.x_dtype}")
     inp = make_inputs(cfg, seed=30 + cid, bias_rand=True)
     nw = _norm_weight(cfg.d, cfg.x_dtype, 7).to(DEV)
     out, route = rt.moe_block(inp.x, nw, 1e-5, inp.router_w, inp.router_b, inp.glu, inp.lin,
