@@ -68,6 +68,17 @@ constexpr int WD_BASE_WAIT = WD_WLOADS + WD_WLOADS * (2 * WD_SP - 3) + WD_ALOADS
 static_assert(WD_BASE_WAIT + WD_TILE_LOADS < 64, "vmcnt range");
 constexpr int wd_wait(int n) { return n < 63 ? n : 63; }
 
+// The lane id, recomputed where it is used. The kernel runs at the 256-VGPR
+// limit; a lane-derived value held across the loop gets spilled, and its
+// reload (the youngest load) costs a wait for every load in flight, which
+// drains the prefetch pipeline. The asm keeps the compiler from keeping or
+// spilling it.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 template <bool OPAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gemm_up_direct(GemmArgs p) {
@@ -143,12 +154,13 @@ void k_gemm_up_direct(GemmArgs p) {
   // last) and constants (128 floats per wavefront, lanes < 32) of tile T
   // into buffer sel: one load instruction each per wavefront.
   auto issue_tile = [&](const Tile &T, int sel) {
-    if (lane < 16) {
-      const int r = 16 * wave + lane;
+    const int ln = fresh_lane();
+    if (ln < 16) {
+      const int r = 16 * wave + ln;
       dma4(pr, (uint32_t)(T.r0 + min(r, T.rows - 1)) * 4u, 0, rowmap0 + sel * (BM * 4) + 64 * wave);
     }
-    if (lane < 32) {
-      const int col = 4 * T.U0 + (wave & 1) * 128 + 4 * lane;
+    if (ln < 32) {
+      const int col = 4 * T.U0 + (wave & 1) * 128 + 4 * ln;
       dma16(cr, ((uint32_t)T.e * (uint32_t)p.N + (uint32_t)col) * 4u, 0,
             consts0 + sel * 4096 + 512 * wave);
     }
@@ -157,19 +169,21 @@ void k_gemm_up_direct(GemmArgs p) {
   // x loads of a step pair (64 k: 128 contiguous bytes, a whole cache line,
   // per row): wavefront w fills rows 16w .. 16w + 15, instruction i rows
   // 16w + 8i + (l >> 3), 8 lanes per row. Rows are 128 bytes in LDS, 16-byte
-  // chunk c of row r at r·128 + (c ^ sw8(r))·16 (the XOR spreads the
-  // fragment reads of 16 rows over the banks), so lane l loads the chunk
-  // that belongs at its position, (l & 7) ^ sw8(r).
+  // chunk c of row r at r·128 + (c ^ (r & 7))·16 (the XOR puts the same
+  // chunk of 8 consecutive rows, which one fragment read takes together, in
+  // 8 different bank groups), so lane l loads the chunk that belongs at its
+  // position, (l & 7) ^ (r & 7).
   struct AOff {
     uint32_t o[WD_ALOADS];
   };
   auto make_aoff = [&](int sel) {
     AOff A;
+    const int ln = fresh_lane();
 #pragma unroll
     for (int i = 0; i < WD_ALOADS; i++) {
-      const int r = 16 * wave + 8 * i + (lane >> 3);
+      const int r = 16 * wave + 8 * i + (ln >> 3);
       const uint32_t srow = (uint32_t)(rowmap[sel][r] / p.a_row_div);
-      A.o[i] = srow * (uint32_t)p.K * 2u + (uint32_t)((lane & 7) ^ sw8(r)) * 16u;
+      A.o[i] = srow * (uint32_t)p.K * 2u + (uint32_t)((ln & 7) ^ (r & 7)) * 16u;
     }
     return A;
   };
@@ -187,10 +201,11 @@ void k_gemm_up_direct(GemmArgs p) {
   // 4h + cb and 4h + cb + 1 of each step; a unit past N reads the last unit
   // (its outputs are never stored).
   auto wptr = [&](const Tile &T) -> const uint8_t * {
-    const int u = min(T.U0 + 8 * wave + usub, N4 - 1);
-    const uint8_t *w = (const uint8_t *)(src ? p.w1 : p.w0);
-    return w + (uint64_t)T.e * slab + (uint64_t)u * (uint64_t)p.K * 4u + (uint32_t)h * 64u +
-           (uint32_t)cb * 16u;
+    const int ln = fresh_lane(), lmf = ln & 31;
+    const int u = min(T.U0 + 8 * wave + ((lmf >> 1) & 7), N4 - 1);
+    const uint8_t *w = (const uint8_t *)((lmf & 1) ? p.w1 : p.w0);
+    return w + (uint64_t)T.e * slab + (uint64_t)u * (uint64_t)p.K * 4u + (uint32_t)(ln >> 5) * 64u +
+           (uint32_t)(2 * (lmf >> 4)) * 16u;
   };
 
   u32x4 wr[WD_NB][2];  // two whole quantW tiles per step, four steps
@@ -220,18 +235,18 @@ void k_gemm_up_direct(GemmArgs p) {
   floatx16 acc[WD_RT][WD_CT];
 
   // x fragments of one slice: rows 32i + lm, chunk 4q + 2h + kk of the
-  // pair's row (q: the step's place in its pair).
-  int arow[WD_RT], asw[WD_RT];
+  // pair's row (q: the step's place in its pair). Row 32i + lm has swizzle
+  // lm & 7 for every i, and (4q + kk) ^ (2h ^ (lm & 7)) splits into a
+  // compile-time and a lane part, so each (q, kk) has one offset per lane
+  // for all four row tiles (i only adds 4096·i, an immediate).
+  uint32_t aoff[4];
 #pragma unroll
-  for (int i = 0; i < WD_RT; i++) {
-    arow[i] = (32 * i + lm) * 128;
-    asw[i] = sw8(32 * i + lm);
-  }
+  for (int qk = 0; qk < 4; qk++)
+    aoff[qk] = (uint32_t)lm * 128u + 16u * (uint32_t)((4 * (qk >> 1) + (qk & 1)) ^ (2 * h) ^ (lm & 7));
   auto read_a = [&](u32x4 (&F)[WD_RT], int stage, int q, int kk) {
-    const uint8_t *st = aring + stage * WD_P_STAGE;
-    const int c = 4 * q + 2 * h + kk;
+    const uint8_t *st = aring + stage * WD_P_STAGE + aoff[2 * q + kk];
 #pragma unroll
-    for (int i = 0; i < WD_RT; i++) F[i] = *(const u32x4 *)(st + arow[i] + ((c ^ asw[i]) * 16));
+    for (int i = 0; i < WD_RT; i++) F[i] = *(const u32x4 *)(st + 4096 * i);
   };
   auto mfma_slice = [&](const u32x4 (&F)[WD_RT], const StepB &w, int kk) {
     half8 bf[WD_CT];
@@ -366,7 +381,6 @@ void k_gemm_up_direct(GemmArgs p) {
       constexpr int BI = decltype(bi)::value;  // ks % 4: odd for odd ks
       const StepB wb = unpack_w(wr[BI]);
       mfma_slice(F0, wb, 0);
-      __builtin_amdgcn_sched_barrier(0);
       int nstage = stage, nq = 1;
       if constexpr ((BI & 1) != 0) {
         // The awaited x loads went out at step ks − 2·SP + 2 (a barrier
@@ -399,16 +413,13 @@ void k_gemm_up_direct(GemmArgs p) {
         nq = 0;
       }
       read_a(F0, nstage, nq, 0);
-      __builtin_amdgcn_sched_barrier(0);
       mfma_slice(F1, wb, 1);
-      __builtin_amdgcn_sched_barrier(0);
       {
         const int b = ks + WD_NB;
         load_w(wr[BI], b >= ksteps && has_next ? wpn : wp,
                b < ksteps ? b : has_next ? b - ksteps : ksteps - 1);
       }
       read_a(F1, nstage, nq, 1);
-      __builtin_amdgcn_sched_barrier(0);
     };
     for (int ks = 0; ks < ksteps; ks += WD_NB) {
       step(ks, std::integral_constant<int, 0>());
