@@ -163,6 +163,9 @@ __device__ __forceinline__ uint32_t swap8(uint32_t v) {
 // each segment end the second half's sums meet the first's in LDS, added as
 // first + second, before the scales, biases and SwiGLU.
 // NWS streams per block; the block has NW = NWS·KS wavefronts.
+// Weight stream buffers per wavefront (loads SK_PD − 1 steps ahead). 6 and 8
+// measured slower at configs 2 and 3 (fewer wavefronts fit), up to 25%.
+constexpr int SK_PD = 4;
 template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS>
 __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(NS == 1 ? 3 : 4))) void k_expert_skinny(
     ExpertKArgs p) {
@@ -269,11 +272,10 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
   };
   for (int c0 = 0; c0 < cnt; c0 += RC) {
     const int rows = min(RC, cnt - c0);
-    WStep b0, b1, b2, b3;
+    WStep wb[SK_PD];
     // The weight stream does not depend on the rows: start it first.
-    issue(0, b0);
-    issue(1, b1);
-    issue(2, b2);
+#pragma unroll
+    for (int j = 0; j < SK_PD - 1; j++) issue(j, wb[j]);
 
     // Stage this chunk's A rows (gathered through perm) in LDS. Each thread
     // moves 16-byte pieces (8 halves or 4 floats), 8 pieces in flight at
@@ -451,18 +453,15 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
       if (s == kbeg + lsteps - 1) finish(seg);
     };
 
-    // Buffers rotate b0 → b1 → b2 → b3 (loads three steps ahead). The loads
+    // SK_PD buffers in rotation (loads SK_PD − 1 steps ahead). The loads
     // are unconditional (past the stream they read zeros); only the
     // computes are guarded.
-    for (int g = 0; g < gsteps; g += 4) {
-      issue(g + 3, b3);
-      compute(g, b0);
-      issue(g + 4, b0);
-      if (g + 1 < gsteps) compute(g + 1, b1);
-      issue(g + 5, b1);
-      if (g + 2 < gsteps) compute(g + 2, b2);
-      issue(g + 6, b2);
-      if (g + 3 < gsteps) compute(g + 3, b3);
+    for (int g = 0; g < gsteps; g += SK_PD) {
+#pragma unroll
+      for (int j = 0; j < SK_PD; j++) {
+        issue(g + j + SK_PD - 1, wb[(j + SK_PD - 1) % SK_PD]);
+        if (j == 0 || g + j < gsteps) compute(g + j, wb[j]);
+      }
     }
     if (PAIRED) {
       // lin wavefront parks its sums; glu wavefront applies the SwiGLU (the
