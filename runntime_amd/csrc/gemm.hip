@@ -714,8 +714,6 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   p.parts = ea.mode == MODE_DOWN && ea.parts == 2 ? 2 : 1;
   p.kpart = ea.K / BK / p.parts;
   p.part_floats = ea.A * ea.N;
-  p.A = ea.A;
-  p.rsum = db.rsum;
   if (p.kpart < 3 * gemm_stages(ea))
     return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: too few steps per K part");
   // Persistent blocks, one per CU (the LDS ring takes a CU), a multiple of 8

@@ -27,8 +27,6 @@ struct GemmArgs {
   int parts;              // K parts (down); part q writes out + q·A·N
   int kpart;              // steps per part
   int part_floats;        // A·N
-  int A;                  // assignments (sorted positions)
-  float *rsum;            // wide up kernel: [3A] row table and row sums (gemm_wide.hip)
 };
 
 // The wide up kernel (gemm_wide.hip): f16 x, K in whole groups of four

@@ -60,7 +60,7 @@ constexpr int WD_CT = 2;                 // columns of each unit per lane
 constexpr int WD_WLOADS = 2;             // weight loads per lane and step
 constexpr int WD_ALOADS = 2;             // x loads per lane and step pair
 constexpr int WD_STORES = WD_RT * 8;     // epilogue stores per lane
-constexpr int WD_TILE_LOADS = 2;         // row table + constants, per wavefront and tile
+constexpr int WD_TILE_LOADS = 2;         // row map + constants, per wavefront and tile
 // Instructions younger than the x loads a barrier waits for (see the
 // pipeline below): the weight loads of their step, then 2·SP − 3 steps,
 // SP − 2 of them with x loads.
@@ -79,62 +79,12 @@ __device__ __forceinline__ int fresh_lane() {
   return l;
 }
 
-// Eight int8 weights as f16 subnormals: bits 0x00 | (w + 128), the value
-// (w + 128)·2^-24 exactly (f16 MFMA inputs keep subnormals on gfx950). Two
-// VALU per four weights (the XOR that makes w + 128, one v_perm per pair),
-// against three for the biased-normal form 1152 + w less 1152, whose extra
-// packed subtraction measured 6-9% of this kernel's time. The bias leaves
-// the MFMA sums as 2^-24·Σ x·(w + 128); the epilogue takes 2^24·acc − 128·Σx
-// with Σx the row's f32 sum (k_row_sums). Against exact products the f32
-// accumulation then carries 128·|Σx| on top of |Σ x·w|: for zero-mean rows
-// (normalised activations) about 1.5× the rounding of the unbiased sum.
-__device__ __forceinline__ half8 cvt_i8x8_sub(uint32_t x0, uint32_t x1) {
-  x0 ^= 0x80808080u;
-  x1 ^= 0x80808080u;
-  const u32x4 r = {__builtin_amdgcn_perm(0u, x0, 0x0C010C00u), __builtin_amdgcn_perm(0u, x0, 0x0C030C02u),
-                   __builtin_amdgcn_perm(0u, x1, 0x0C010C00u), __builtin_amdgcn_perm(0u, x1, 0x0C030C02u)};
-  return __builtin_bit_cast(half8, r);
-}
-
-// Σ_k x[t, k] in f32 for each source row t (one wavefront per row: lane l
-// sums its 16-byte chunks l, l + 64, … in ascending order, then an xor
-// butterfly), into rsum[2A + t].
-__global__ __launch_bounds__(256) void k_row_sums(const _Float16 *__restrict__ x, int T, int K,
-                                                  float *__restrict__ rsum, int A) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
-  if (t >= T) return;
-  const _Float16 *row = x + (int64_t)t * K;
-  float s = 0.f;
-  for (int k = 8 * lane; k < K; k += 8 * WAVE) {
-    const half8 v = *(const half8 *)(row + k);
-#pragma unroll
-    for (int j = 0; j < 8; j++) s += (float)v[j];
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
-  if (lane == 0) rsum[2 * A + t] = s;
-}
-
-// The kernel's row table, per sorted position p: {perm[p], the sum of its
-// source row perm[p] / div}, in rsum[2p], rsum[2p + 1].
-__global__ __launch_bounds__(256) void k_sorted_sums(const int32_t *__restrict__ perm, int A, int div,
-                                                     float *__restrict__ rsum) {
-  const int p = blockIdx.x * 256 + threadIdx.x;
-  if (p < A) {
-    const int a = perm[p];
-    rsum[2 * p] = __builtin_bit_cast(float, a);
-    rsum[2 * p + 1] = rsum[2 * A + a / div];
-  }
-}
-
 template <bool OPAIR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gemm_up_direct(GemmArgs p) {
   __shared__ __align__(16) uint8_t aring[WD_SP * WD_P_STAGE];
   __shared__ __align__(16) uint8_t junk[1024];  // target of the placeholder loads
-  // Per tile row: {assignment, Σ_k x of its source row (f32 bits)}.
-  __shared__ __align__(16) int32_t rowtab[2][2 * BM];
+  __shared__ __align__(16) int32_t rowmap[2][BM];
   // Epilogue constants per tile: glu scales, lin scales, glu biases, lin
   // biases (256 each).
   __shared__ __align__(16) float consts[2][1024];
@@ -187,28 +137,28 @@ void k_gemm_up_direct(GemmArgs p) {
 
   const uint32_t aring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)aring;
   const uint32_t junk0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)junk;
-  const uint32_t rowtab0 =
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t *)&rowtab[0][0];
+  const uint32_t rowmap0 =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t *)&rowmap[0][0];
   const uint32_t consts0 =
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)&consts[0][0];
   const uint64_t slab = (uint64_t)p.K * (uint64_t)p.N;  // weight bytes of one expert
   const i32x4 ar = buffer_rsrc(p.a, (uint32_t)p.a_bytes);
-  const i32x4 tr = buffer_rsrc(p.rsum, (uint32_t)p.A * 8u);
+  const i32x4 pr = buffer_rsrc(p.perm, (uint32_t)p.perm_bytes);
   // Wavefronts 2a, 2a + 1 load constant array a (glu scales, lin scales,
   // glu biases, lin biases), halves wave & 1; a missing bias reads zeros
   // from an empty buffer.
   const float *cbase = wave < 2 ? p.s0 : wave < 4 ? p.s1 : wave < 6 ? p.b0 : p.b1;
   const i32x4 cr = buffer_rsrc(cbase, cbase ? (uint32_t)p.E * (uint32_t)p.N * 4u : 0u);
 
-  // Row table (rows 16·wave .. + 15, two per lane, lanes < 8) and constants
-  // (128 floats per wavefront, lanes < 32) of tile T into buffer sel: one
-  // load instruction each per wavefront. Rows past the tile read the next
-  // tile's entries, or zeros (assignment 0) past the table: valid rows to
-  // gather, whose outputs are never stored.
+  // Row map (rows 16·wave + lane, lanes < 16; rows past the tile repeat its
+  // last) and constants (128 floats per wavefront, lanes < 32) of tile T
+  // into buffer sel: one load instruction each per wavefront.
   auto issue_tile = [&](const Tile &T, int sel) {
     const int ln = fresh_lane();
-    if (ln < 8)
-      dma16(tr, (uint32_t)(T.r0 + 16 * wave + 2 * ln) * 8u, 0, rowtab0 + sel * (BM * 8) + 128 * wave);
+    if (ln < 16) {
+      const int r = 16 * wave + ln;
+      dma4(pr, (uint32_t)(T.r0 + min(r, T.rows - 1)) * 4u, 0, rowmap0 + sel * (BM * 4) + 64 * wave);
+    }
     if (ln < 32) {
       const int col = 4 * T.U0 + (wave & 1) * 128 + 4 * ln;
       dma16(cr, ((uint32_t)T.e * (uint32_t)p.N + (uint32_t)col) * 4u, 0,
@@ -232,7 +182,7 @@ void k_gemm_up_direct(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < WD_ALOADS; i++) {
       const int r = 16 * wave + 8 * i + (ln >> 3);
-      const uint32_t srow = (uint32_t)(rowtab[sel][2 * r] / p.a_row_div);
+      const uint32_t srow = (uint32_t)(rowmap[sel][r] / p.a_row_div);
       A.o[i] = srow * (uint32_t)p.K * 2u + (uint32_t)((ln & 7) ^ (r & 7)) * 16u;
     }
     return A;
@@ -300,10 +250,10 @@ void k_gemm_up_direct(GemmArgs p) {
   };
   auto mfma_slice = [&](const u32x4 (&F)[WD_RT], const StepB &w, int kk) {
     half8 bf[WD_CT];
-    bf[0] = cvt_i8x8_sub(w.b[kk][0][0], w.b[kk][0][1]);
+    bf[0] = cvt_i8x8(w.b[kk][0][0], w.b[kk][0][1]);
 #pragma unroll
     for (int c = 0; c < WD_CT; c++) {
-      if (c + 1 < WD_CT) bf[c + 1] = cvt_i8x8_sub(w.b[kk][c + 1][0], w.b[kk][c + 1][1]);
+      if (c + 1 < WD_CT) bf[c + 1] = cvt_i8x8(w.b[kk][c + 1][0], w.b[kk][c + 1][1]);
 #pragma unroll
       for (int i = 0; i < WD_RT; i++)
         acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, F[i]), bf[c],
@@ -324,10 +274,7 @@ void k_gemm_up_direct(GemmArgs p) {
                                          (~m & __builtin_bit_cast(uint32_t, y)));
   };
   auto epilogue = [&](const Tile &T, int sel) {
-    // Lane values recomputed here rather than held through the loop.
-    const int eln = fresh_lane(), elm = eln & 31, h = eln >> 5;
-    const int usub = (elm >> 1) & 7, cb = 2 * (elm >> 4);
-    const bool low = (elm & 1) == 0;
+    const bool low = src == 0;
     const uint32_t lowm = low ? ~0u : 0u;
     const int uo = T.U0 + 8 * wave + usub;
     const bool col_ok = uo < N4;
@@ -339,11 +286,6 @@ void k_gemm_up_direct(GemmArgs p) {
     for (int i = 0; i < WD_RT; i++)
 #pragma unroll
       for (int r = 0; r < 8; r++) {
-        const int rr = low ? r : r + 8;
-        const int row = 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-        // The products accumulated (w + 128)·2^-24 per weight (see
-        // cvt_i8x8_sub): x·w = 2^24·acc − 128·Σ_k x.
-        const float corr = 128.0f * __builtin_bit_cast(float, rowtab[sel][2 * row + 1]);
         float v[WD_CT];
 #pragma unroll
         for (int c = 0; c < WD_CT; c++) {
@@ -351,11 +293,13 @@ void k_gemm_up_direct(GemmArgs p) {
           const float send = pick(lowm, a8, a0);
           const float recv = __builtin_bit_cast(
               float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, true));
-          const float g = pick(lowm, a0, recv) * 16777216.0f - corr;
-          const float l = pick(lowm, recv, a8) * 16777216.0f - corr;
+          const float g = pick(lowm, a0, recv);
+          const float l = pick(lowm, recv, a8);
           v[c] = swiglu(g * sg[c] + bg[c], l * sl[c] + bl[c]);
         }
-        const uint32_t orow = p.sorted ? (uint32_t)(T.r0 + row) : (uint32_t)rowtab[sel][2 * row];
+        const int rr = low ? r : r + 8;
+        const int row = 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
+        const uint32_t orow = p.sorted ? (uint32_t)(T.r0 + row) : (uint32_t)rowmap[sel][row];
         const uint32_t off = (row < T.rows && col_ok)
                                  ? (orow * (uint32_t)p.N + 4u * uo + (uint32_t)cb) * 4u
                                  : 0x80000000u;
@@ -471,11 +415,9 @@ void k_gemm_up_direct(GemmArgs p) {
       read_a(F0, nstage, nq, 0);
       mfma_slice(F1, wb, 1);
       {
-        // Past the tile: the next tile's first steps (on the last tile wpn
-        // is wp, and steps 0-3 are re-read).
         const int b = ks + WD_NB;
-        const bool over = b >= ksteps;
-        load_w(wr[BI], over ? wpn : wp, over ? b - ksteps : b);
+        load_w(wr[BI], b >= ksteps && has_next ? wpn : wp,
+               b < ksteps ? b : has_next ? b - ksteps : ksteps - 1);
       }
       read_a(F1, nstage, nq, 1);
     };
@@ -508,14 +450,6 @@ bool gemm_wide_eligible(const ExpertArgs &ea) {
 }
 
 int launch_gemm_up_wide(const GemmArgs &p, int blocks, bool pairs, hipStream_t s) {
-  MOE_NONNULL(p.rsum);
-  const int T = p.A / p.a_row_div;
-  if (p.K % 8 != 0 || (int64_t)T * p.K * 2 > (int64_t)p.a_bytes)
-    return moe_fail(MOE_EXECUTION_FAILED, "gemm up: x rows do not match the assignments");
-  hipLaunchKernelGGL(k_row_sums, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s,
-                     (const _Float16 *)p.a, T, p.K, p.rsum, p.A);
-  hipLaunchKernelGGL(k_sorted_sums, dim3((unsigned)((p.A + 255) / 256)), dim3(256), 0, s, p.perm, p.A,
-                     p.a_row_div, p.rsum);
   dim3 grid((unsigned)blocks), block(WD_WAVES * WAVE);
   if (pairs) hipLaunchKernelGGL((k_gemm_up_direct<true>), grid, block, 0, s, p);
   else hipLaunchKernelGGL((k_gemm_up_direct<false>), grid, block, 0, s, p);

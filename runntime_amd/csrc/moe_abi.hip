@@ -308,7 +308,6 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   size_t o_act_list = p.take(sizeof(int32_t) * C * 4 * E);
   size_t o_meta = p.take(sizeof(int32_t) * C * META_N);
   size_t o_perm = p.take(sizeof(int32_t) * C * A);
-  size_t o_rsum = p.take(sizeof(float) * C * 3 * A);
   size_t o_route = p.take(sizeof(float) * C * route_floats);
   size_t o_part = p.take(sizeof(float) * C * partial_floats);
   size_t o_actv = p.take(sizeof(float) * C * act_floats);
@@ -334,7 +333,6 @@ static int plan_ws(moe_ctx *ctx, int calls, int T, int k, int E, size_t route_fl
   L.db.active = (int32_t *)(b + o_act_list);
   L.db.meta = (int32_t *)(b + o_meta);
   L.db.perm = (int32_t *)(b + o_perm);
-  L.db.rsum = (float *)(b + o_rsum);
   L.db.E = E;
   L.db.A = A;
   L.db.nblk = nblk;

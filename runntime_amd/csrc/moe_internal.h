@@ -113,10 +113,6 @@ struct DispatchBufs {
                         // experts with rows, ascending; then {-1, 0, 0, 0}
   int32_t *meta;        // [META_N] per call
   int32_t *perm;        // [A] per call: sorted position → assignment
-  // [3A] per call: the wide up GEMM's row table, {assignment, f32 row sum
-  // of x} per sorted position in [0, 2A), and the sums per source row from
-  // 2A on.
-  float *rsum;
   int E, A, nblk;       // sizes that give the per-call strides
   __host__ __device__ int64_t cnt_cs() const { return (int64_t)nblk * E; }
   __host__ __device__ int64_t off_cs() const { return (int64_t)E + 1; }
