@@ -169,10 +169,11 @@ void k_gemm_up_direct(GemmArgs p) {
   // x loads of a step pair (64 k: 128 contiguous bytes, a whole cache line,
   // per row): wavefront w fills rows 16w .. 16w + 15, instruction i rows
   // 16w + 8i + (l >> 3), 8 lanes per row. Rows are 128 bytes in LDS, 16-byte
-  // chunk c of row r at r·128 + (c ^ (r & 7))·16 (the XOR puts the same
-  // chunk of 8 consecutive rows, which one fragment read takes together, in
-  // 8 different bank groups), so lane l loads the chunk that belongs at its
-  // position, (l & 7) ^ (r & 7).
+  // chunk c of row r at r·128 + (c ^ sw8(r))·16. A 16-byte fragment read is
+  // served 16 lanes (16 rows) at a time; sw8 gives 16 consecutive rows 16
+  // different 16-byte bank positions (r & 7 alone repeats after 8 rows and
+  // measured 5e7 bank-conflict cycles per config-4 launch). Lane l loads the
+  // chunk that belongs at its position, (l & 7) ^ sw8(r).
   struct AOff {
     uint32_t o[WD_ALOADS];
   };
@@ -183,7 +184,7 @@ void k_gemm_up_direct(GemmArgs p) {
     for (int i = 0; i < WD_ALOADS; i++) {
       const int r = 16 * wave + 8 * i + (ln >> 3);
       const uint32_t srow = (uint32_t)(rowmap[sel][r] / p.a_row_div);
-      A.o[i] = srow * (uint32_t)p.K * 2u + (uint32_t)((ln & 7) ^ (r & 7)) * 16u;
+      A.o[i] = srow * (uint32_t)p.K * 2u + (uint32_t)((ln & 7) ^ sw8(r)) * 16u;
     }
     return A;
   };
@@ -236,17 +237,18 @@ void k_gemm_up_direct(GemmArgs p) {
 
   // x fragments of one slice: rows 32i + lm, chunk 4q + 2h + kk of the
   // pair's row (q: the step's place in its pair). Row 32i + lm has swizzle
-  // lm & 7 for every i, and (4q + kk) ^ (2h ^ (lm & 7)) splits into a
-  // compile-time and a lane part, so each (q, kk) has one offset per lane
-  // for all four row tiles (i only adds 4096·i, an immediate).
+  // sw8(lm) ^ 4·(i & 1), and (4q + kk) ^ 2h ^ sw8(lm) splits into a
+  // compile-time and a lane part: each (q, kk) has one offset per lane,
+  // odd row tiles take (q ^ 1, kk)'s, and i adds 4096·i, an immediate.
   uint32_t aoff[4];
 #pragma unroll
   for (int qk = 0; qk < 4; qk++)
-    aoff[qk] = (uint32_t)lm * 128u + 16u * (uint32_t)((4 * (qk >> 1) + (qk & 1)) ^ (2 * h) ^ (lm & 7));
+    aoff[qk] = (uint32_t)lm * 128u + 16u * (uint32_t)((4 * (qk >> 1) + (qk & 1)) ^ (2 * h) ^ sw8(lm));
   auto read_a = [&](u32x4 (&F)[WD_RT], int stage, int q, int kk) {
-    const uint8_t *st = aring + stage * WD_P_STAGE + aoff[2 * q + kk];
+    const uint8_t *st0 = aring + stage * WD_P_STAGE + aoff[2 * q + kk];
+    const uint8_t *st1 = aring + stage * WD_P_STAGE + aoff[2 * (q ^ 1) + kk];
 #pragma unroll
-    for (int i = 0; i < WD_RT; i++) F[i] = *(const u32x4 *)(st + 4096 * i);
+    for (int i = 0; i < WD_RT; i++) F[i] = *(const u32x4 *)(((i & 1) ? st1 : st0) + 4096 * i);
   };
   auto mfma_slice = [&](const u32x4 (&F)[WD_RT], const StepB &w, int kk) {
     half8 bf[WD_CT];
