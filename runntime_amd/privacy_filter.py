@@ -265,62 +265,63 @@ class ViterbiBiases:
     end_to_start: float = 0.0
 
 
+# The decoder's moves, as a table: (group of the previous label, role of the
+# next label) → the ViterbiBiases field added to an allowed move (None: 0).
+# Roles: "O" background (its span class is the background one, or it is the
+# background token), "B"/"I"/"E"/"S" a boundary tag of a span class, "X" a
+# label without a span class or without a tag, "Z" a span class with a tag
+# other than B/I/E/S. Groups of the previous label: "O"; "BI" (inside a span:
+# only I or E of the same span class may follow); "ES" (a span just ended);
+# "X" (may start anything, with no bias); "Z" (nothing may follow). Any pair
+# not listed, and any next label of role "X" or "Z", is not allowed.
+_MOVES = {
+    ("O", "O"): "background_stay", ("O", "B"): "background_to_start",
+    ("O", "S"): "background_to_start",
+    ("ES", "O"): "end_to_background", ("ES", "B"): "end_to_start", ("ES", "S"): "end_to_start",
+    ("X", "O"): None, ("X", "B"): None, ("X", "S"): None,
+    ("BI", "I"): "inside_to_continue", ("BI", "E"): "inside_to_end",
+}
+_GROUP = {"O": "O", "B": "BI", "I": "BI", "E": "ES", "S": "ES", "X": "X", "Z": "Z"}
+
+
 class ViterbiDecoder:
     """The constrained BIOES decoder (viterbi.ts:20-148): start/end scores
     and a transition matrix of allowed moves (−1e9 elsewhere) with the
-    optional biases; ties keep the lower previous label."""
+    optional biases; ties keep the lower previous label. The allowed moves
+    and their biases are the table above; the reference states the same
+    rules as nested conditions (viterbi.ts:20-82)."""
     NEG_INF = -1e9
 
     def __init__(self, info: LabelInfo, biases: Optional[ViterbiBiases] = None):
         b = biases or ViterbiBiases()
         n = info.num_classes
         self.n = n
-        tag = lambda i: info.token_boundary_tags.get(i)
-        span = lambda i: info.token_to_span_label.get(i)
-        is_bg = lambda i: span(i) == info.background_span_label or i == info.background_token_label
+        cls = [info.token_to_span_label.get(i) for i in range(n)]
 
-        def valid(p, q):
-            q_bg, qt = is_bg(q), tag(q)
-            if (span(q) is None or qt is None) and not q_bg:
-                return False
-            pt = tag(p)
-            if span(p) is None or pt is None or is_bg(p) or pt in ("E", "S"):
-                return q_bg or qt in ("B", "S")
-            if pt in ("B", "I"):
-                return span(p) == span(q) and qt in ("I", "E")
-            return False
+        tags = [info.token_boundary_tags.get(i) for i in range(n)]
 
-        def bias(p, q):
-            pt, qt = tag(p), tag(q)
-            if is_bg(p):
-                if is_bg(q):
-                    return b.background_stay
-                return b.background_to_start if qt in ("B", "S") else 0.0
-            if pt in ("B", "I"):
-                if qt == "I" and span(p) == span(q):
-                    return b.inside_to_continue
-                if qt == "E" and span(p) == span(q):
-                    return b.inside_to_end
-                return 0.0
-            if pt in ("E", "S"):
-                if is_bg(q):
-                    return b.end_to_background
-                return b.end_to_start if qt in ("B", "S") else 0.0
-            return 0.0
+        def role(i):
+            if cls[i] == info.background_span_label or i == info.background_token_label:
+                return "O"
+            if cls[i] is None or tags[i] is None:
+                return "X"
+            return tags[i] if tags[i] in ("B", "I", "E", "S") else "Z"
 
+        roles = [role(i) for i in range(n)]
         bg = info.background_token_label
-        self.start = np.full(n, self.NEG_INF, dtype=np.float64)
-        self.end = np.full(n, self.NEG_INF, dtype=np.float64)
+        starts = {i for i in range(n) if tags[i] in ("B", "S") or i == bg}
+        ends = {i for i in range(n) if tags[i] in ("E", "S") or i == bg}
+        self.start = np.array([0.0 if i in starts else self.NEG_INF for i in range(n)])
+        self.end = np.array([0.0 if i in ends else self.NEG_INF for i in range(n)])
         self.trans = np.full((n, n), self.NEG_INF, dtype=np.float64)
-        for i in range(n):
-            t = tag(i)
-            if t in ("B", "S") or i == bg:
-                self.start[i] = 0.0
-            if t in ("E", "S") or i == bg:
-                self.end[i] = 0.0
-            for j in range(n):
-                if valid(i, j):
-                    self.trans[i, j] = bias(i, j)
+        for p in range(n):
+            g = _GROUP[roles[p]]
+            for q in range(n):
+                key = (g, roles[q])
+                if key not in _MOVES or (g == "BI" and cls[p] != cls[q]):
+                    continue
+                field = _MOVES[key]
+                self.trans[p, q] = getattr(b, field) if field else 0.0
 
     def decode(self, log_probs: np.ndarray) -> List[int]:
         """The library's native decode (moe_viterbi_decode): ties keep the
@@ -346,41 +347,39 @@ class TokenSpan:
 
 
 def labels_to_spans(labels, info: LabelInfo) -> List[TokenSpan]:
-    """labelsToSpans (spans.ts:18-70)."""
-    spans, cur, start = [], [None], [None]
+    """labelsToSpans (spans.ts:18-70): token spans from BIOES labels. One
+    open span at a time; labels with no span class are skipped, background
+    closes the open span, B opens one, I continues the open span of its
+    class (or opens one), E closes the open span of its class (or stands
+    alone), S stands alone; whatever is open at the end is closed there."""
+    out: List[TokenSpan] = []
+    open_span = None  # (span class, first token)
 
-    def flush(end_excl):
-        if cur[0] is not None and start[0] is not None:
-            spans.append(TokenSpan(cur[0], start[0], end_excl))
-        cur[0], start[0] = None, None
+    def close(at):
+        nonlocal open_span
+        if open_span is not None:
+            out.append(TokenSpan(open_span[0], open_span[1], at))
+        open_span = None
 
-    for idx, lab in enumerate(labels):
-        sl = info.token_to_span_label.get(lab)
-        tag = info.token_boundary_tags.get(lab)
-        if sl is None:
+    for i, lab in enumerate(labels):
+        c = info.token_to_span_label.get(lab)
+        if c is None:
             continue
-        if sl == info.background_span_label:
-            flush(idx)
-            continue
-        if tag == "S":
-            flush(idx)
-            spans.append(TokenSpan(sl, idx, idx + 1))
-        elif tag == "B":
-            flush(idx)
-            cur[0], start[0] = sl, idx
-        elif tag == "I":
-            if cur[0] is None or cur[0] != sl:
-                flush(idx)
-                cur[0], start[0] = sl, idx
-        elif tag == "E":
-            if cur[0] is None or cur[0] != sl or start[0] is None:
-                flush(idx)
-                spans.append(TokenSpan(sl, idx, idx + 1))
-            else:
-                spans.append(TokenSpan(cur[0], start[0], idx + 1))
-                cur[0], start[0] = None, None
-    flush(len(labels))
-    return spans
+        kind = "O" if c == info.background_span_label else info.token_boundary_tags.get(lab)
+        same = open_span is not None and open_span[0] == c
+        if kind == "O":
+            close(i)
+        elif kind == "B" or (kind == "I" and not same):
+            close(i)
+            open_span = (c, i)
+        elif kind == "E" and same:
+            out.append(TokenSpan(c, open_span[1], i + 1))
+            open_span = None
+        elif kind in ("E", "S"):
+            close(i)
+            out.append(TokenSpan(c, i, i + 1))
+    close(len(labels))
+    return out
 
 
 # ------------------------------------------------------------------ loading
