@@ -166,7 +166,10 @@ __device__ __forceinline__ uint32_t swap8(uint32_t v) {
 // Weight stream buffers per wavefront (loads SK_PD − 1 steps ahead). 6 and 8
 // measured slower at configs 2 and 3 (fewer wavefronts fit), up to 25%.
 constexpr int SK_PD = 4;
-template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS>
+// NORM: gate/up of moe_block with the pre-norm applied while staging
+// (a_inv, a_normw); a template flag, so that the instances without it keep
+// their registers.
+template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS, bool NORM = false>
 __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(NS == 1 ? 3 : 4))) void k_expert_skinny(
     ExpertKArgs p) {
   constexpr int NW = NWS * KS;
@@ -289,10 +292,16 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
       const int total = RC * cpr;
       const int srcv = lane < rows ? perm[p0 + c0 + lane] / p.a_row_div : 0;
       const bool vec = p.K % EPC == 0 && (((uintptr_t)abase) & 15) == 0;
-      for (int b0 = threadIdx.x; b0 < total; b0 += 8 * NT) {
-        u32x4 v[8];
+      const AT *nw = (const AT *)p.a_normw;
+      const bool nvec = vec && (((uintptr_t)nw) & 15) == 0;
+      // Pieces per batch: 8, or 4 with the norm's weights and inverse RMS
+      // loaded alongside.
+      constexpr int PB = NORM ? 4 : 8;
+      for (int b0 = threadIdx.x; b0 < total; b0 += PB * NT) {
+        u32x4 v[PB], nwv[NORM ? PB : 1];
+        float invv[NORM ? PB : 1];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < PB; u++) {
           const int c = b0 + u * NT;
           const int r = c < total ? c / cpr : 0;
           const int k = (c - r * cpr) * EPC;
@@ -307,21 +316,40 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
             for (int j = 0; j < EPC; j++) e[j] = (ok && k + j < p.K) ? xr[k + j] : (AT)0;
             v[u] = __builtin_bit_cast(u32x4, e);
           }
-          if (p.a_normw) {
-            // moe_block's pre-norm while staging: x·inv·w in f32, rounded
-            // to x's dtype, as the standalone norm stores it.
-            const AT *nw = (const AT *)p.a_normw;
-            const float inv = ok ? p.a_inv[src] : 0.f;
-            AT e[EPC];
+          if constexpr (NORM) {
+            // The norm's weights and the row's inverse RMS, loaded with x.
+            invv[u] = ok ? p.a_inv[src] : 0.f;
+            if (nvec) {
+              nwv[u] = (ok && k < p.K) ? *(const u32x4 *)(nw + k) : u32x4{0, 0, 0, 0};
+            } else {
+              AT e[EPC];
+#pragma unroll
+              for (int j = 0; j < EPC; j++) e[j] = (ok && k + j < p.K) ? nw[k + j] : (AT)0;
+              nwv[u] = __builtin_bit_cast(u32x4, e);
+            }
+          }
+        }
+        if constexpr (NORM) {
+          // moe_block's pre-norm while staging: x·inv·w in f32, rounded to
+          // x's dtype, as the standalone norm stores it (after every load of
+          // the batch is out).
+#pragma unroll
+          for (int u = 0; u < PB; u++) {
+            const int c = b0 + u * NT;
+            const int r = c < total ? c / cpr : 0;
+            const int k = (c - r * cpr) * EPC;
+            const bool ok = c < total && r < rows;
+            AT e[EPC], wn[EPC];
             __builtin_memcpy(e, &v[u], sizeof(e));
+            __builtin_memcpy(wn, &nwv[u], sizeof(wn));
 #pragma unroll
             for (int j = 0; j < EPC; j++)
-              if (ok && k + j < p.K) e[j] = (AT)moe_dev::norm_value<AT>((float)e[j], inv, (float)nw[k + j]);
+              if (ok && k + j < p.K) e[j] = (AT)moe_dev::norm_value<AT>((float)e[j], invv[u], (float)wn[j]);
             v[u] = __builtin_bit_cast(u32x4, e);
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < PB; u++) {
           const int c = b0 + u * NT;
           if (c >= total) break;
           const int r = c / cpr, k = (c - r * cpr) * EPC;
@@ -694,7 +722,15 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
     const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, ks == 2 ? nw : 0);
 #define SKINNY(AT_, GR_, NW_, NS_, KS_)                                                   \
-  hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_, KS_>), grid, block, lds, s, q)
+  do {                                                                                    \
+    if constexpr (MODE == MODE_UP) {                                                      \
+      if (q.a_normw) {                                                                    \
+        hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_, KS_, true>), grid, block, lds, s, q); \
+        break;                                                                            \
+      }                                                                                   \
+    }                                                                                     \
+    hipLaunchKernelGGL((k_expert_skinny<MODE, AT_, GR_, NW_, NS_, KS_>), grid, block, lds, s, q); \
+  } while (0)
 #define SKINNY_KS(AT_, GR_, NW_, NS_)                                                     \
   if constexpr (!GR_) {                                                                   \
     if (ks == 2) { SKINNY(AT_, GR_, NW_, NS_, 2); } else { SKINNY(AT_, GR_, NW_, NS_, 1); } \

@@ -607,10 +607,12 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   LayerWs L;
   const size_t esize = x_dtype == MOE_F16 ? 2 : 4;
   // The pre-norm: folded into the router's and the skinny gate/up kernel's
-  // staging (the router's chunk kernel leaves each token's inverse RMS in
-  // the xn slot), or, for the grouped GEMM (loads straight into LDS), a
+  // staging for calls of at most FUSED_T tokens (the router's chunk kernel
+  // computes and leaves each token's inverse RMS in the xn slot); for larger
+  // calls (the register-tiled router, whose many blocks per token tile would
+  // each recompute it) and for the grouped GEMM (loads straight into LDS), a
   // normalised copy xn.
-  const bool stage_norm = norm && expert_stages_norm(up);
+  const bool stage_norm = norm && T <= FUSED_T && expert_stages_norm(up);
   if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
                     router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L,
                     norm ? (stage_norm ? (size_t)T * 4 : (size_t)T * d * esize) : 0, fixed)))

@@ -53,6 +53,30 @@ __global__ __launch_bounds__(256) void k_topk(const T *__restrict__ logits, int 
 constexpr int RT_TOKENS = 16;
 constexpr int RT_EXPERTS = 128;
 
+// Inverse RMS of 1-4 rows (x, x + stride, …) in the canonical order, their
+// loads issued together (wave_rows_inv) for rows up to 2048 long.
+template <typename T>
+__device__ __forceinline__ void tile_rows_inv(const T *x, int64_t stride, int count, int n, float eps,
+                                              int lane, float (&inv)[4]) {
+  if (n <= 256) {
+    moe_dev::wave_rows_inv<T, 4, 1>(x, stride, count, n, eps, lane, inv);
+  } else if (n <= 512) {
+    moe_dev::wave_rows_inv<T, 4, 2>(x, stride, count, n, eps, lane, inv);
+  } else if (n <= 1024) {
+    moe_dev::wave_rows_inv<T, 4, 4>(x, stride, count, n, eps, lane, inv);
+  } else if (n <= 2048) {
+    float a[2], b[2];
+    moe_dev::wave_rows_inv<T, 2, 8>(x, stride, min(count, 2), n, eps, lane, a);
+    b[0] = b[1] = 0.f;
+    if (count > 2) moe_dev::wave_rows_inv<T, 2, 8>(x + 2 * stride, stride, count - 2, n, eps, lane, b);
+    inv[0] = a[0], inv[1] = a[1], inv[2] = b[0], inv[3] = b[1];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      inv[r] = r < count ? moe_dev::wave_row_inv(x + r * stride, n, eps, lane) : 0.f;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   __shared__ float xs[RT_TOKENS * ROUTER_CHUNK];
@@ -70,34 +94,17 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   const int et = min(RT_EXPERTS, E - e0);
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
-  // moe_block's pre-norm: each wavefront takes the inverse RMS of four of
-  // the tile's tokens (the canonical order); the first chunk's blocks store it.
-  __shared__ float sinv[RT_TOKENS];
-  const T *nw = (const T *)ra.norm_w;
-  if (nw) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    for (int tt = threadIdx.x / WAVE; tt < RT_TOKENS; tt += 256 / WAVE) {
-      const int t = t0 + tt;
-      if (t >= Tn) break;
-      const float inv = moe_dev::wave_row_inv(x + (int64_t)t * d, d, ra.norm_eps, lane);
-      if (lane == 0) {
-        sinv[tt] = inv;
-        if (j == 0 && blockIdx.z % etiles == 0) ra.inv[t] = inv;
-      }
-    }
-    __syncthreads();
-  }
   // Staging: every load of the tile is issued before the first LDS store.
   constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
-  float xv[XPER], wv[WPER];
+  const T *nw = (const T *)ra.norm_w;
+  float xv[XPER], wv[WPER], nv[XPER];
 #pragma unroll
   for (int r = 0; r < XPER; r++) {
     int i = threadIdx.x + 256 * r;
     int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
     int t = t0 + tt;
     xv[r] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
-    if (nw && t < Tn && kk < len)
-      xv[r] = moe_dev::norm_value<T>(xv[r], sinv[tt], load_as_f32(nw, k0 + kk));
+    nv[r] = (nw && kk < len) ? load_as_f32(nw, k0 + kk) : 0.f;
   }
 #pragma unroll
   for (int r = 0; r < WPER; r++) {
@@ -105,6 +112,39 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
     int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
     wv[r] = (kk < len && ee < et) ? __builtin_nontemporal_load(w + (int64_t)(k0 + kk) * E + e0 + ee)
                                   : 0.f;
+  }
+  // moe_block's pre-norm, while the tile's loads are in flight: wavefront w
+  // takes the inverse RMS of the tile's tokens w, w + 4, w + 8, w + 12 (the
+  // canonical order), the loads of all four rows out at once; the first
+  // chunk's blocks store it.
+  static_assert(RT_TOKENS == 4 * (256 / WAVE), "four tokens per wavefront");
+  __shared__ float sinv[RT_TOKENS];
+  if (nw) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w4 = threadIdx.x / WAVE;
+    const int count = min(4, max(0, (Tn - t0 - w4 + 3) / 4));
+    float inv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (count > 0) tile_rows_inv(x + (int64_t)(t0 + w4) * d, 4 * (int64_t)d, count, d, ra.norm_eps, lane, inv);
+    if (lane == 0) {
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        if (b >= count) break;
+        const int tt = w4 + 4 * b;
+        sinv[tt] = inv[b];
+        if (j == 0 && blockIdx.z % etiles == 0) ra.inv[t0 + tt] = inv[b];
+      }
+    }
+    __syncthreads();
+  }
+  // The pre-norm after every load of the tile is out (a norm right after
+  // its load would wait for that load before the next one went out).
+  if (nw) {
+#pragma unroll
+    for (int r = 0; r < XPER; r++) {
+      int i = threadIdx.x + 256 * r;
+      int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
+      if (t0 + tt < Tn && kk < len) xv[r] = moe_dev::norm_value<T>(xv[r], sinv[tt], nv[r]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < XPER; r++) xs[threadIdx.x + 256 * r] = xv[r];
@@ -299,22 +339,6 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
   const int tid = threadIdx.x;
-  // moe_block's pre-norm (as k_router_chunks): the tile's inverse RMS values.
-  __shared__ float sinv[TB];
-  const T *nw = (const T *)ra.norm_w;
-  if (nw) {
-    const int lane = tid & (WAVE - 1);
-    for (int tt = tid / WAVE; tt < TB; tt += 256 / WAVE) {
-      const int t = t0 + tt;
-      if (t >= Tn) break;
-      const float inv = moe_dev::wave_row_inv(x + (int64_t)t * d, d, ra.norm_eps, lane);
-      if (lane == 0) {
-        sinv[tt] = inv;
-        if (j == 0 && blockIdx.z % etiles == 0) ra.inv[t] = inv;
-      }
-    }
-    __syncthreads();
-  }
   // Staging in 16-byte loads where the chunk is whole and aligned: x as
   // 8-element runs of a token's row (stored transposed), W as 4-expert runs.
   const bool vec = len == ROUTER_CHUNK && (d & 7) == 0 && (E & 3) == 0 && e0 + EB <= E;
@@ -338,10 +362,6 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
 #pragma unroll
         for (int q = 0; q < 8; q++) v[q] = 0.f;
       }
-      if (nw && t < Tn) {
-#pragma unroll
-        for (int q = 0; q < 8; q++) v[q] = moe_dev::norm_value<T>(v[q], sinv[tt], load_as_f32(nw, k0 + kk + q));
-      }
 #pragma unroll
       for (int q = 0; q < 8; q++) xs[(kk + q) * TB + tt] = v[q];
     }
@@ -352,9 +372,7 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   } else {
     for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
       const int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK, t = t0 + tt;
-      float v = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
-      if (nw && t < Tn && kk < len) v = moe_dev::norm_value<T>(v, sinv[tt], load_as_f32(nw, k0 + kk));
-      xs[kk * TB + tt] = v;
+      xs[kk * TB + tt] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
     }
     for (int i = tid; i < ROUTER_CHUNK * EB; i += 256) {
       const int kk = i / EB, ee = i % EB, e = e0 + ee;
@@ -422,6 +440,8 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
   const bool fuse = db && ra.T <= FUSED_T && ra.T * ra.k <= FUSED_T * MAX_K;
   // Many tokens: the register-tiled chunk kernel (64 or 32 experts a block).
   if (!fuse && ra.T > SMALL_T && ra.E >= 32) {
+    if (ra.norm_w)
+      return moe_fail(MOE_EXECUTION_FAILED, "router: the staged pre-norm runs on calls of at most 64 tokens");
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
     if (ra.E >= 64) {
       const int tb = 4 * (256 / (64 / 4)), et = (ra.E + 63) / 64;
