@@ -77,7 +77,9 @@ __device__ __forceinline__ void tile_rows_inv(const T *x, int64_t stride, int co
   }
 }
 
-template <typename T>
+// NORM: moe_block's pre-norm applied while staging (ra.norm_w); a template
+// flag, so that the plain instance keeps its few registers (occupancy).
+template <typename T, bool NORM>
 __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   __shared__ float xs[RT_TOKENS * ROUTER_CHUNK];
   __shared__ float ws[ROUTER_CHUNK * RT_EXPERTS];
@@ -96,15 +98,15 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   const int len = min(ROUTER_CHUNK, d - k0);
   // Staging: every load of the tile is issued before the first LDS store.
   constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
-  const T *nw = (const T *)ra.norm_w;
-  float xv[XPER], wv[WPER], nv[XPER];
+  const T *nw = NORM ? (const T *)ra.norm_w : nullptr;
+  float xv[XPER], wv[WPER], nv[NORM ? XPER : 1];
 #pragma unroll
   for (int r = 0; r < XPER; r++) {
     int i = threadIdx.x + 256 * r;
     int tt = i / ROUTER_CHUNK, kk = i % ROUTER_CHUNK;
     int t = t0 + tt;
     xv[r] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
-    nv[r] = (nw && kk < len) ? load_as_f32(nw, k0 + kk) : 0.f;
+    if constexpr (NORM) nv[r] = kk < len ? load_as_f32(nw, k0 + kk) : 0.f;
   }
 #pragma unroll
   for (int r = 0; r < WPER; r++) {
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   // chunk's blocks store it.
   static_assert(RT_TOKENS == 4 * (256 / WAVE), "four tokens per wavefront");
   __shared__ float sinv[RT_TOKENS];
-  if (nw) {
+  if constexpr (NORM) {
     const int lane = threadIdx.x & (WAVE - 1);
     const int w4 = threadIdx.x / WAVE;
     const int count = min(4, max(0, (Tn - t0 - w4 + 3) / 4));
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   }
   // The pre-norm after every load of the tile is out (a norm right after
   // its load would wait for that load before the next one went out).
-  if (nw) {
+  if constexpr (NORM) {
 #pragma unroll
     for (int r = 0; r < XPER; r++) {
       int i = threadIdx.x + 256 * r;
@@ -458,10 +460,13 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
     const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
     dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
-    if (ra.x_dtype == MOE_F16)
-      hipLaunchKernelGGL(k_router_chunks<_Float16>, grid, block, 0, s, ra);
-    else
-      hipLaunchKernelGGL(k_router_chunks<float>, grid, block, 0, s, ra);
+    if (ra.x_dtype == MOE_F16) {
+      if (ra.norm_w) hipLaunchKernelGGL((k_router_chunks<_Float16, true>), grid, block, 0, s, ra);
+      else hipLaunchKernelGGL((k_router_chunks<_Float16, false>), grid, block, 0, s, ra);
+    } else {
+      if (ra.norm_w) hipLaunchKernelGGL((k_router_chunks<float, true>), grid, block, 0, s, ra);
+      else hipLaunchKernelGGL((k_router_chunks<float, false>), grid, block, 0, s, ra);
+    }
   }
   const int ni = (ra.E + WAVE - 1) / WAVE;
   // Fold batch: the chunk count J, rounded up to 8, 16 or 32 (8 with more
