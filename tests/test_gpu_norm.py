@@ -145,3 +145,25 @@ def test_moe_block_is_norm_then_layer(cid, T, x_dtype):
     diff = np.argwhere(a != b)
     assert len(diff) == 0, [(i, j, a[i, j], b[i, j]) for i, j in diff[:8]]
     assert np.array_equal(host(out), host(o2))
+
+
+@pytest.mark.parametrize("T,d,x_dtype", [(33, 200, "f16"), (10, 2304, None)])
+def test_moe_block_staged_norm_row_lengths(T, d, x_dtype):
+    """The router's staged pre-norm reads a wavefront's rows together for
+    rows of up to 2048 elements (shorter rows in fewer loads per lane) and
+    row by row beyond; both stay bit-identical to rmsNorm → moe_layer. T = 33
+    leaves the last token tile one token, so most wavefronts have none."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS[3], T=T, d=d, E=16, I=256)
+    if x_dtype:
+        cfg = dataclasses.replace(cfg, x_dtype=x_dtype)
+    say(f"moe_block staged norm T={T} d={d} {cfg.x_dtype}")
+    inp = make_inputs(cfg, seed=40 + d, bias_rand=True)
+    nw = _norm_weight(cfg.d, cfg.x_dtype, 9).to(DEV)
+    out, route = rt.moe_block(inp.x, nw, 1e-5, inp.router_w, inp.router_b, inp.glu, inp.lin,
+                              inp.down, cfg.k, return_route=True)
+    xn = rt.rmsNorm(inp.x, nw, 1e-5)
+    o2, r2 = rt.moe_layer(xn, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                          inp.x.float().contiguous(), cfg.k, return_route=True)
+    assert np.array_equal(host(route), host(r2))
+    assert np.array_equal(host(out), host(o2))
