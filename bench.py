@@ -552,7 +552,24 @@ def main():
                     "kernel": "k_gemm_up_direct (gate/up grouped GEMM + SwiGLU)",
                     "algorithmic_flops_per_launch": fl, "avg_launch_us": round(up_avg_s * 1e6, 2)}
         layer_frac = layer_flops(cfg) * calls / (ms_per_step / 1e3) / 1e12 / MFMA_F16_PEAK_TFLOPS
+        # The down product (k_gemm_down_i8: three int8 MFMAs per product on
+        # act's int8 limbs), against the same f16 peak in algorithmic flops.
+        dn_ms, dn_n = groups.get("down", (0.0, 0))
+        dn_fl = cfg.T * cfg.k * 2 * cfg.d * cfg.I
+        dn_avg_s = dn_ms / max(dn_n, 1) / 1e3
+        roofline["down"] = {"kernel": "k_gemm_down_i8 (down grouped GEMM, int8 MFMA on act limbs)",
+                            "algorithmic_flops_per_launch": dn_fl,
+                            "avg_launch_us": round(dn_avg_s * 1e6, 2),
+                            "achieved": round(dn_fl / dn_avg_s / 1e12, 2),
+                            "frac": round(dn_fl / dn_avg_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
 
+    rows = None
+    if args.config in (4, 5):
+        r = rt.router_topk(sets[0].x, sets[0].router_w, sets[0].router_b, cfg.k)
+        cnt = torch.bincount(r[:, :cfg.k].reshape(-1).long(), minlength=cfg.E)
+        rows = {"min": int(cnt.min()), "max": int(cnt.max()),
+                "experts_without_rows": int((cnt == 0).sum()),
+                "hottest_share_of_tokens": round(int(cnt.max()) / cfg.T, 4)}
     line = {
         "metric": "MoE-layer tokens/s at 1 MI355X",
         "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -567,8 +584,13 @@ def main():
                                      else (args.c3_calls or args.copies) if args.config == 3
                                      else 1),
                    "graph": graph is not None, "parallelism": "single GPU",
-                   "arith": "int8 weights exact in f16 MFMA, f32 inputs split hi+lo, f32 accumulate"},
+                   "arith": ("int8 weights exact in f16 MFMA, f32 accumulate; act between the "
+                             "prefill products as 24-bit fixed point in three int8 limbs on "
+                             "int8 MFMA, i32 accumulate" if args.config in (4, 5) else
+                             "int8 weights exact in f16 MFMA, f32 inputs split hi+lo, "
+                             "f32 accumulate")},
         "layer_roofline_frac": round(layer_frac, 4),
+        **({"rows_per_expert": rows} if rows else {}),
         "kernel_ms": {g: round(ms / n, 5) for g, (ms, n) in groups.items()},
         "roofline": roofline,
         "source_sha": source_sha(),

@@ -27,7 +27,7 @@ PER_FILE = {
     "router.hip": ["-ffp-contract=off"],
     "norm.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "gemm_wide.hip", "pack.hip", "norm.hip", "float.hip", "attn.hip", "linear.hip"]
+SOURCES = ["moe_abi.hip", "router.hip", "dispatch.hip", "expert.hip", "gemm.hip", "gemm_wide.hip", "gemm_i8.hip", "pack.hip", "norm.hip", "float.hip", "attn.hip", "linear.hip"]
 
 
 # Host-only C++ (no device code), compiled by the host compiler.

@@ -687,6 +687,11 @@ int gemm_down_parts(const ExpertArgs &ea) {
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   if (ea.calls != 1)
     return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: one call per launch");
+  if (ea.act_i8 && ea.mode == MODE_DOWN) {
+    const int cus = gemm_cus();
+    if (cus <= 0) return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: no CU count for the device");
+    return launch_gemm_down_i8(ea, db, cus, s);
+  }
   GemmArgs p;
   p.a = ea.a;
   p.a_row_div = ea.a_row_div;
@@ -714,6 +719,13 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   p.parts = ea.mode == MODE_DOWN && ea.parts == 2 ? 2 : 1;
   p.kpart = ea.K / BK / p.parts;
   p.part_floats = ea.A * ea.N;
+  p.act_i8 = ea.act_i8;
+  p.act_npairs = ea.N / 64;
+  if (ea.act_i8) {
+    if (ea.mode != MODE_UP || !gemm_wide_eligible(ea) || ea.N % 64)
+      return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: int8-limb act needs the f16-x up GEMM");
+    p.out_bytes = (int)gemm_i8_act_bytes(ea.A, ea.E, ea.N);
+  }
   if (p.kpart < 3 * gemm_stages(ea))
     return moe_fail(MOE_EXECUTION_FAILED, "expert gemm: too few steps per K part");
   // Persistent blocks, one per CU (the LDS ring takes a CU), a multiple of 8
@@ -731,7 +743,8 @@ int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t
   // of steps.
   const bool pair = p.kpart % 2 == 0;
   // Up with f16 x: weights straight into registers (gemm_wide.hip).
-  if (gemm_wide_eligible(ea)) return launch_gemm_up_wide(p, (int)blocks, pairs, s);
+  if (gemm_wide_eligible(ea))
+    return launch_gemm_up_wide(p, (int)blocks, ea.act_i8 ? 2 : pairs ? 1 : 0, s);
 #define LAUNCH_P(M_, AT_, OP_)                                                            \
   do {                                                                                    \
     if (pair) hipLaunchKernelGGL((k_expert_gemm<M_, AT_, OP_, true>), grid, block, 0, s, p); \

@@ -27,12 +27,17 @@ struct GemmArgs {
   int parts;              // K parts (down); part q writes out + q·A·N
   int kpart;              // steps per part
   int part_floats;        // A·N
+  int act_i8;             // up: write act as int8 limbs (gemm_i8.hip's layout)
+  int act_npairs;         // up with act_i8: N / 64
 };
 
 // The wide up kernel (gemm_wide.hip): f16 x, K in whole groups of four
 // steps and at least 16 steps.
 bool gemm_wide_eligible(const ExpertArgs &ea);
-int launch_gemm_up_wide(const GemmArgs &p, int blocks, bool pairs, hipStream_t s);
+// omode: 0 f32 act, 1 f16 hi + lo pairs, 2 int8 limbs (gemm_i8.hip).
+int launch_gemm_up_wide(const GemmArgs &p, int blocks, int omode, hipStream_t s);
+// The down product of the fused layer on the int8 matrix cores (gemm_i8.hip).
+int launch_gemm_down_i8(const ExpertArgs &dn, const DispatchBufs &db, int cus, hipStream_t s);
 
 namespace {
 
@@ -154,6 +159,7 @@ struct Tile {
   int U0, U1;  // first unit of each weight source
   int part;  // K part
   int kb;    // first step of the part
+  int mtg;   // global index of the M-tile (padded rows 128·mtg ..)
 };
 
 

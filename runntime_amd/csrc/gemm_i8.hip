@@ -1,0 +1,408 @@
+// Grouped down GEMM of the fused prefill layer on the int8 matrix cores.
+//
+// Reference: src/core/kernels/matmul/moeQuantW.ts:188-237 (moeDown: the
+// routed act rows times the expert's int8 down weights, per-column scale and
+// bias); quantW layout src/core/kernels/quantCommon.ts:8-31.
+//
+// act between the two products is private to the layer. The gate/up GEMM
+// writes every f32 act value v as the 24-bit fixed-point integer
+// V = rint(v · 2^17) (|act| ≤ 56 by the clamped SwiGLU, so |V| < 2^23; the
+// rounding error, 2^-18 absolute, is three orders below the f16 hi + lo
+// split's contribution to the 2e-3 output bar), stored as three signed
+// bytes with V = 65536·h + 256·m + l. Down then runs three exact
+// v_mfma_i32_32x32x32_i8 per product (limbs h, m, l against the int8
+// weights, i32 accumulation: |Σ| ≤ 128·127·K, below 2^31 for K < 132,000)
+// and adds the limbs in the epilogue in f32. Against the f16 hi + lo form
+// this is 3 int8 MFMAs (each half an f16 MFMA's time) instead of 4 f16 per
+// 32 k, and the weights feed the matrix cores as loaded: no int8 → f16
+// conversion at all.
+//
+// The limbs: W = V + 32896 as a 24-bit two's complement integer has bytes
+// b0, b1, b2; l = b0 ^ 0x80 and m = b1 ^ 0x80 read as signed bytes are
+// b0 − 128 and b1 − 128, and h = b2 (signed), so l + 256·m + 65536·h =
+// W − 32896 = V.
+//
+// act layout (bytes), over padded rows: the sorted row p of expert e sits
+// at padded row P = 128·(first M-tile of e) + (p − first row of e), so each
+// 64-row block of P holds rows of one expert. Block b, pair of steps j
+// (64 k), limb L, step q of the pair, 16-k half hf: a 1 KB chunk of 64 rows
+// × 16 bytes (k = 64j + 32q + 16hf + 0..15, in order) at
+//   ((b·(K/64) + j)·12 + (2L + q)·2 + hf)·1024 + (P mod 64)·16.
+// A pair of a block is one contiguous 12 KB run: its direct-to-LDS loads
+// are whole lines, and its LDS image is the MFMA A fragments as they are
+// read (16 lanes read 256 contiguous bytes).
+//
+// Tiles: 64 rows (one act block) × 128 units (512 columns) per block of four
+// wavefronts, one per SIMD. Wavefront w takes all 64 rows and units
+// 32w .. 32w + 31: 2 row tiles × 4 column tiles × 3 limbs = 24 MFMAs and 384
+// i32 accumulators (in AGPRs and VGPRs). Lane l = 32hf + u holds unit u of
+// the wavefront for k half hf; per step it loads the unit's 64 contiguous
+// bytes for its half (four quantW tiles of 4 columns × 4 k), and column c's
+// dwords of the four tiles are the B operand of column tile c (columns
+// 4u + c): no exchange between lanes. act comes through an LDS ring of step
+// pairs; the weights straight into registers, two steps ahead.
+//
+// Order of tiles: expert, then N-tile, then 64-row block, cut into 8
+// contiguous ranges, one per XCD (block b runs on XCD b mod 8), so the
+// blocks of an (expert, N-tile) — which share its weights — and the N-tiles
+// of a row block — which share its act — run at once on one L2.
+#include "gemm_dev.h"
+
+#include <type_traits>
+
+namespace {
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int I8_WAVES = 4;
+constexpr int I8_BM = 64;                        // rows per tile (one act block)
+constexpr int I8_UNITS = 128;                    // weight units per tile
+constexpr int I8_SPA = 4;                        // act ring stages (step pairs)
+constexpr int I8_SPW = 3;                        // weight ring stages (step pairs)
+constexpr int I8_PAIR = I8_BM * 64 * 3;          // act bytes of one pair: 12 KB
+constexpr int I8_DMA = I8_PAIR / 1024 / I8_WAVES;  // act loads per wavefront and pair: 3
+constexpr int I8_WPAIR = I8_WAVES * 2 * 32 * 128;  // weights of one pair: 32 KB
+constexpr int I8_MAX_E = GEMM_MAX_E;
+
+struct I8Args {
+  const uint8_t *act;      // limbs, layout above
+  uint32_t act_bytes;
+  const uint8_t *w;        // quantW words of the down weight [E·K, N]
+  const float *scales;     // [E, N]
+  const float *bias;       // [E, N] or NULL
+  float *y;                // [A, N] f32, row = assignment
+  uint32_t y_bytes;
+  const int32_t *perm;     // sorted position → assignment
+  const int32_t *active;   // [E][4] {e, first row, rows, first M-tile}
+  const int32_t *meta;
+  int K, N, E;
+  int nt;                  // N-tiles (512 columns each)
+};
+
+// acc += A·B on the int8 matrix cores. Limbs h and m accumulate in AGPRs,
+// limb l in VGPRs: 384 accumulators do not fit the 256 VGPRs, and an asm
+// operand class keeps the register allocator from moving them between the
+// two files (with the builtin it spills and copies them). The compiler does
+// not see into the asm, so the hazards it would cover are covered here: the
+// B operand is assembled by VALU moves just before, and an MFMA may read a
+// VGPR a VALU instruction wrote only 2 wait states later (s_nop 2 gives 3);
+// the results are read only after drain_mfma().
+template <int L3>
+__device__ __forceinline__ void mfma_i8(i32x16 &acc, i32x4 a, i32x4 b, std::integral_constant<int, L3>) {
+  if constexpr (L3 < 2)
+    asm volatile("s_nop 2\n\tv_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("s_nop 2\n\tv_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+// Wait states between the last MFMA and the first read of its result (a
+// 16-pass XDL result is readable 18 wait states after issue).
+__device__ __forceinline__ void drain_mfma() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+__device__ __forceinline__ int fresh_lane_i8() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemm_down_i8(I8Args p) {
+  __shared__ __align__(16) uint8_t aring[I8_SPA * I8_PAIR];  // 48 KB
+  __shared__ __align__(16) uint8_t wring[I8_SPW * I8_WPAIR];  // 96 KB
+  __shared__ __align__(16) uint8_t junk[1024];
+  __shared__ int32_t rowmap[I8_BM];
+  __shared__ int4 descs[I8_MAX_E];
+  __shared__ int c64[I8_MAX_E + 1];  // cumulative 64-row blocks per active expert
+
+  const int n_active = p.meta[META_ACTIVE];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n_active; i += blockDim.x) descs[i] = ((const int4 *)p.active)[i];
+  __syncthreads();
+  if (tid < 64) {
+    // One wavefront scans the per-expert block counts (ceil(rows / 64)).
+    int carry = 0;
+    for (int base = 0; base < n_active; base += 64) {
+      const int i = base + tid;
+      int v = i < n_active ? (descs[i].z + I8_BM - 1) / I8_BM : 0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(v, o, 64);
+        if (tid >= o) v += t;
+      }
+      if (i < n_active) c64[i + 1] = carry + v;
+      carry += __shfl(v, 63, 64);
+    }
+    if (tid == 0) c64[0] = 0;
+  }
+  __syncthreads();
+  const int total = c64[n_active] * p.nt;
+  const int bx = gridDim.x >> 3;
+  const int xcd = blockIdx.x & 7, xb = blockIdx.x >> 3;
+  const int per_x = (total + 7) >> 3;
+  const int start = xcd * per_x + xb, end = min(total, (xcd + 1) * per_x);
+
+  const int lane = tid & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+  const int hf = lane >> 5, u = lane & 31;
+  const int N4 = p.N / 4;
+  const int ksteps = p.K / BK, npairs = ksteps / 2;
+  const uint64_t slab = (uint64_t)p.K * (uint64_t)p.N;
+  const i32x4 ar = buffer_rsrc(p.act, p.act_bytes);
+  const uint32_t aring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)aring;
+  const uint32_t junk0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)junk;
+  const uint32_t wring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)wring;
+  const __amdgpu_buffer_rsrc_t yrc = __builtin_amdgcn_make_buffer_rsrc(p.y, 0, p.y_bytes, BUF_DWORD3);
+
+  for (int L = start; L < end; L += bx) {
+    // ---- the tile: expert (binary search over the block counts), N-tile,
+    // row block.
+    int lo = 0, hi = n_active - 1;
+    // Tiles of active expert i: c64[i]·nt .. c64[i + 1]·nt.
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (c64[mid] * p.nt <= L) lo = mid; else hi = mid - 1;
+    }
+    const int4 d = descs[lo];
+    const int nb = c64[lo + 1] - c64[lo];
+    const int local = L - c64[lo] * p.nt;
+    const int ntile = local / nb, jb = local % nb;
+    const int e = __builtin_amdgcn_readfirstlane(d.x);
+    const int r0 = __builtin_amdgcn_readfirstlane(d.y + jb * I8_BM);  // first sorted row
+    const int rows = __builtin_amdgcn_readfirstlane(min(I8_BM, d.z - jb * I8_BM));
+    const int blk = __builtin_amdgcn_readfirstlane(2 * d.w + jb);    // act block
+    const int U0 = ntile * I8_UNITS;
+
+    if (tid < I8_BM) rowmap[tid] = p.perm[r0 + min(tid, rows - 1)];
+
+    // act pair j of this block: 12 chunks of 1 KB; wavefront w loads chunks
+    // 3w .. 3w + 2, lane l bytes 16l of each (whole lines).
+    const uint32_t a_base = (uint32_t)blk * (uint32_t)npairs * (uint32_t)I8_PAIR;
+    auto issue_a = [&](int j, int stage) {
+      const int ln = fresh_lane_i8();
+#pragma unroll
+      for (int i = 0; i < I8_DMA; i++) {
+        const int c = I8_DMA * wave + i;
+        dma16(ar, a_base + (uint32_t)j * I8_PAIR + (uint32_t)c * 1024u + (uint32_t)ln * 16u, 0,
+              aring0 + stage * I8_PAIR + c * 1024);
+      }
+    };
+    // Placeholder loads (into a junk LDS area) keep the per-pair count of
+    // vector memory instructions constant in the prologue and past the end.
+    auto issue_junk = [&](int n) {
+      for (int i = 0; i < n; i++) dma16(ar, 0u, 0, junk0);
+    };
+    // Weights of pair j (steps 2j, 2j + 1) for wavefront w's 32 units, by
+    // direct-to-LDS loads of whole lines: instruction (q, i) loads units
+    // 8i .. 8i + 7 of the wavefront, lane l the 16-byte chunk
+    // (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes of step 2j + q,
+    // so that chunk c of unit u sits at u·128 + (c ^ sw8(u))·16: the 16
+    // lanes reading one tile of 16 units hit 16 different bank groups. A unit
+    // past N reads the last unit (its outputs are not stored).
+    const int unit_last = N4 - 1;
+    const i32x4 wr = buffer_rsrc(p.w + (uint64_t)e * slab, (uint32_t)slab);
+    uint32_t woff[4];
+    {
+      const int ln = fresh_lane_i8();
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int uu = 8 * i + (ln >> 3);
+        const int ug = min(U0 + 32 * wave + uu, unit_last);
+        woff[i] = (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u;
+      }
+    }
+    auto issue_w = [&](int j, int stage) {
+#pragma unroll
+      for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          dma16(wr, woff[i], (2 * j + q) * (BK * 4),
+                wring0 + stage * I8_WPAIR + wave * 8192 + q * 4096 + i * 1024);
+    };
+
+    i32x16 acc[2][4][3];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int l3 = 0; l3 < 3; l3++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[i][c][l3][r] = 0;
+
+    // The pipeline. Frags of a step are read from LDS during the previous
+    // step's MFMAs. In the middle of pair j (between its two steps) every
+    // wavefront waits for pair j + 1's loads and a barrier follows: then all
+    // of pair j's LDS has been read, so the act loads of pair j + SPA and the
+    // weight loads of pair j + SPW go into pair j's stages (3 + 8 per
+    // wavefront, 11 vector memory instructions per pair), and pair j + 1's
+    // first frags are read. At the wait, pair j + 1's weights (issued one
+    // pair after its act) are followed by exactly one pair's 11 younger
+    // instructions. The prologue issues virtual pairs −SPA .. −1 of the same
+    // pattern (placeholders where a pair is out of range).
+    static_assert(I8_SPA == I8_SPW + 1, "act runs one pair ahead of the weights");
+#pragma unroll
+    for (int v = 0; v < I8_SPA; v++) {
+      if (v < npairs) issue_a(v, v);
+      else issue_junk(I8_DMA);
+      const int jw = v - 1;
+      if (jw >= 0 && jw < npairs) issue_w(jw, jw);
+      else issue_junk(8);
+    }
+
+    // Fragments of step q of the pair in LDS stages sa (act), sw (weights):
+    // act of row tile rt, limb l3 for half hf; the weight unit's four tiles
+    // for half hf (tile t = column 0..3 × k 4t .. 4t + 3).
+    struct Frags {
+      u32x4 a[2][3];
+      u32x4 w[4];
+    };
+    const int swu = sw8(u);
+    auto read_frags = [&](Frags &F, int sa, int sw, int q) {
+      const uint8_t *s = aring + sa * I8_PAIR + hf * 1024 + u * 16 + q * 2048;
+#pragma unroll
+      for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int l3 = 0; l3 < 3; l3++) F.a[rt][l3] = *(const u32x4 *)(s + l3 * 4096 + rt * 512);
+      const uint8_t *t = wring + sw * I8_WPAIR + wave * 8192 + q * 4096 + u * 128;
+#pragma unroll
+      for (int j4 = 0; j4 < 4; j4++) F.w[j4] = *(const u32x4 *)(t + ((hf * 4 + j4) ^ swu) * 16);
+    };
+    // MFMAs of one step; hook(slot) runs after each of the 8 groups of three.
+    auto mfmas = [&](const Frags &F, auto hook) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        // Column c's dwords of the four quantW tiles: 16 k of column 4u + c.
+        const i32x4 B = {(int)F.w[0][c], (int)F.w[1][c], (int)F.w[2][c], (int)F.w[3][c]};
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+          mfma_i8(acc[rt][c][0], __builtin_bit_cast(i32x4, F.a[rt][0]), B, std::integral_constant<int, 0>());
+          mfma_i8(acc[rt][c][1], __builtin_bit_cast(i32x4, F.a[rt][1]), B, std::integral_constant<int, 1>());
+          mfma_i8(acc[rt][c][2], __builtin_bit_cast(i32x4, F.a[rt][2]), B, std::integral_constant<int, 2>());
+          hook(2 * c + rt);
+        }
+      }
+    };
+    auto no_hook = [](int) {};
+    // Load number n (0..10) of a pair's 11: act chunks 0-2, then the weight
+    // instructions (q, i) in order. Branch-free: past the last pair the
+    // load goes to the junk area (a load under a branch makes the compiler
+    // wait for every load in flight where the paths join).
+    auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
+      if (n < I8_DMA) {
+        const bool ok = ja < npairs;
+        const int c = I8_DMA * wave + n;
+        const uint32_t at = a_base + (uint32_t)ja * I8_PAIR + (uint32_t)c * 1024u +
+                            (uint32_t)fresh_lane_i8() * 16u;
+        const uint32_t voff = ok ? at : 0u;
+        dma16(ar, voff, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
+      } else {
+        const bool ok = jw < npairs;
+        const int t = n - I8_DMA, q = t >> 2, i = t & 3;
+        dma16(wr, woff[i], ok ? (2 * jw + q) * (BK * 4) : 0,
+              ok ? wring0 + sw_ * I8_WPAIR + wave * 8192 + q * 4096 + i * 1024 : junk0);
+      }
+    };
+
+    // Pair 0's loads: its weights are followed by two virtual pairs' 22.
+    WAIT_VMCNT(2 * (I8_DMA + 8));
+    block_barrier();
+    Frags Fa, Fb;
+    read_frags(Fa, 0, 0, 0);
+    int sa = 0, sw = 0;
+    for (int j = 0; j < npairs; j++) {
+      read_frags(Fb, sa, sw, 1);
+      mfmas(Fa, no_hook);
+      WAIT_VMCNT(I8_DMA + 8);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      block_barrier();
+      // This pair's stages are free: the loads of pairs j + SPA (act) and
+      // j + SPW (weights) go there, spread between the MFMA groups of the
+      // step below (all wavefronts issuing them in one burst stalls the
+      // matrix cores of the CU together).
+      const int ja = j + I8_SPA, jw = j + I8_SPW, sa0 = sa, sw0 = sw;
+      sa = sa + 1 == I8_SPA ? 0 : sa + 1;
+      sw = sw + 1 == I8_SPW ? 0 : sw + 1;
+      // (past the last pair this reads a stage that holds no pair: unused)
+      read_frags(Fa, sa, sw, 0);
+      mfmas(Fb, [&](int slot) {
+        issue_one(slot, ja, sa0, jw, sw0);
+        if (slot < 3) issue_one(slot + 8, ja, sa0, jw, sw0);
+      });
+    }
+    WAIT_VMCNT(0);
+    drain_mfma();
+    block_barrier();
+
+    // ---- epilogue: y[assignment][col .. col + 3] = scale · V-sum · 2^-17
+    // + bias, for columns 4·unit' + 0..3 of the lane.
+    const int uo = U0 + 32 * wave + u;
+    const bool col_ok = uo < N4;
+    const int col = 4 * min(uo, N4 - 1);
+    const floatx4 sc = *(const floatx4 *)(p.scales + (size_t)e * p.N + col) * (1.0f / 131072.0f);
+    floatx4 bs = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) bs = *(const floatx4 *)(p.bias + (size_t)e * p.N + col);
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = 32 * rt + 8 * (r / 4) + 4 * hf + (r % 4);
+        floatx4 o;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          float v = (float)acc[rt][c][0][r] * 65536.0f;
+          v = __builtin_fmaf((float)acc[rt][c][1][r], 256.0f, v);
+          v += (float)acc[rt][c][2][r];
+          o[c] = __builtin_fmaf(v, sc[c], bs[c]);
+        }
+        const uint32_t off = (row < rows && col_ok)
+                                 ? ((uint32_t)rowmap[row] * (uint32_t)p.N + (uint32_t)col) * 4u
+                                 : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), yrc, off, 0, 0);
+      }
+    // rowmap is rewritten by the next tile.
+    block_barrier();
+  }
+}
+
+}  // namespace
+
+bool gemm_i8_down_eligible(const ExpertArgs &dn) {
+  // 8-bit weights with one scale group per column, K in whole step pairs
+  // with at least a ring's worth of them, 32-bit buffer offsets.
+  const int64_t mt = (dn.A + BM - 1) / BM + (dn.E < dn.A ? dn.E : dn.A);
+  return dn.mode == MODE_DOWN && dn.bits == 8 && dn.g == dn.K && dn.K % 64 == 0 &&
+         dn.K / 64 >= I8_SPA && dn.N % 4 == 0 && dn.E <= I8_MAX_E && dn.calls == 1 &&
+         gemm_i8_act_bytes(dn.A, dn.E, dn.K) < (1ll << 31) &&
+         (int64_t)dn.A * dn.N * 4 < (1ll << 31) && (int64_t)dn.K * dn.N < (1ll << 31) &&
+         mt > 0;
+}
+
+int64_t gemm_i8_act_bytes(int A, int E, int K) {
+  const int64_t mt = (A + BM - 1) / BM + (E < A ? E : A);
+  return mt * BM * (int64_t)K * 3;
+}
+
+int launch_gemm_down_i8(const ExpertArgs &dn, const DispatchBufs &db, int cus, hipStream_t s) {
+  I8Args p;
+  p.act = (const uint8_t *)dn.a;
+  p.act_bytes = (uint32_t)gemm_i8_act_bytes(dn.A, dn.E, dn.K);
+  p.w = (const uint8_t *)dn.w0.w;
+  p.scales = dn.w0.scales;
+  p.bias = dn.w0.bias;
+  p.y = dn.out;
+  p.y_bytes = (uint32_t)((int64_t)dn.A * dn.N * 4);
+  p.perm = db.perm;
+  p.active = db.active;
+  p.meta = db.meta;
+  p.K = dn.K;
+  p.N = dn.N;
+  p.E = dn.E;
+  p.nt = (dn.N + 511) / 512;
+  long blocks = ((long)(dn.A + I8_BM - 1) / I8_BM + dn.E) * p.nt;
+  if (blocks > cus) blocks = cus;
+  blocks = (blocks + 7) / 8 * 8;
+  hipLaunchKernelGGL(k_gemm_down_i8, dim3((unsigned)blocks), dim3(I8_WAVES * WAVE), 0, s, p);
+  return 0;
+}

@@ -79,7 +79,7 @@ __device__ __forceinline__ int fresh_lane() {
   return l;
 }
 
-template <bool OPAIR>
+template <int OMODE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void k_gemm_up_direct(GemmArgs p) {
   __shared__ __align__(16) uint8_t aring[WD_SP * WD_P_STAGE];
@@ -132,6 +132,7 @@ void k_gemm_up_direct(GemmArgs p) {
     T.U0 = T.U1 = __builtin_amdgcn_readfirstlane(ntile * 64);
     T.part = 0;
     T.kb = 0;
+    T.mtg = __builtin_amdgcn_readfirstlane(d.w + mtile);
     return T;
   };
 
@@ -301,22 +302,45 @@ void k_gemm_up_direct(GemmArgs p) {
         }
         const int rr = low ? r : r + 8;
         const int row = 32 * i + 8 * (rr / 4) + 4 * h + (rr % 4);
-        const uint32_t orow = p.sorted ? (uint32_t)(T.r0 + row) : (uint32_t)rowmap[sel][row];
-        const uint32_t off = (row < T.rows && col_ok)
-                                 ? (orow * (uint32_t)p.N + 4u * uo + (uint32_t)cb) * 4u
-                                 : 0x80000000u;
-        u32x2 o;
-        if constexpr (OPAIR) {
-          // The f32 pair's 8 bytes as hi(n), hi(n + 1), lo(n), lo(n + 1).
-          const _Float16 h0 = (_Float16)v[0], h1 = (_Float16)v[1];
-          o[0] = __builtin_bit_cast(uint32_t, half2v{h0, h1});
-          o[1] = __builtin_bit_cast(
-              uint32_t, half2v{(_Float16)(v[0] - (float)h0), (_Float16)(v[1] - (float)h1)});
+        const bool ok = row < T.rows && col_ok;
+        if constexpr (OMODE == 2) {
+          // int8 limbs of V = rint(v·2^17) (gemm_i8.hip): padded row
+          // P = 128·mtg + row, k = 4·uo + cb (even) and k + 1.
+          const uint32_t P = 128u * (uint32_t)T.mtg + (uint32_t)row;
+          const uint32_t k = 4u * (uint32_t)uo + (uint32_t)cb;
+          const uint32_t base =
+              ((P >> 6) * (uint32_t)p.act_npairs + (k >> 6)) * 12288u + ((k >> 5) & 1u) * 2048u +
+              ((k >> 4) & 1u) * 1024u + (P & 63u) * 16u + (k & 15u);
+          uint32_t w[WD_CT];
+#pragma unroll
+          for (int c = 0; c < WD_CT; c++)
+            w[c] = (uint32_t)((int)__builtin_rintf(fminf(fmaxf(v[c], -63.5f), 63.5f) * 131072.0f) +
+                              32896);
+          // limbs h = b2, m = b1 ^ 0x80, l = b0 ^ 0x80, at L·4096.
+          const uint32_t hh = ((w[0] >> 16) & 0xffu) | (((w[1] >> 16) & 0xffu) << 8);
+          const uint32_t mm = (((w[0] >> 8) & 0xffu) | (((w[1] >> 8) & 0xffu) << 8)) ^ 0x8080u;
+          const uint32_t ll = ((w[0] & 0xffu) | ((w[1] & 0xffu) << 8)) ^ 0x8080u;
+          const uint32_t o0 = ok ? base : 0x80000000u;
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hh, orc, o0, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)mm, orc, ok ? base + 4096u : o0, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)ll, orc, ok ? base + 8192u : o0, 0, 0);
         } else {
-          o[0] = __builtin_bit_cast(uint32_t, v[0]);
-          o[1] = __builtin_bit_cast(uint32_t, v[1]);
+          const uint32_t orow = p.sorted ? (uint32_t)(T.r0 + row) : (uint32_t)rowmap[sel][row];
+          const uint32_t off = ok ? (orow * (uint32_t)p.N + 4u * uo + (uint32_t)cb) * 4u
+                                  : 0x80000000u;
+          u32x2 o;
+          if constexpr (OMODE == 1) {
+            // The f32 pair's 8 bytes as hi(n), hi(n + 1), lo(n), lo(n + 1).
+            const _Float16 h0 = (_Float16)v[0], h1 = (_Float16)v[1];
+            o[0] = __builtin_bit_cast(uint32_t, half2v{h0, h1});
+            o[1] = __builtin_bit_cast(
+                uint32_t, half2v{(_Float16)(v[0] - (float)h0), (_Float16)(v[1] - (float)h1)});
+          } else {
+            o[0] = __builtin_bit_cast(uint32_t, v[0]);
+            o[1] = __builtin_bit_cast(uint32_t, v[1]);
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(o, orc, off, 0, 0);
         }
-        __builtin_amdgcn_raw_buffer_store_b64(o, orc, off, 0, 0);
       }
   };
 
@@ -451,9 +475,10 @@ bool gemm_wide_eligible(const ExpertArgs &ea) {
          ea.K / BK >= 4 * WD_SP && (ea.K / BK) % WD_NB == 0;
 }
 
-int launch_gemm_up_wide(const GemmArgs &p, int blocks, bool pairs, hipStream_t s) {
+int launch_gemm_up_wide(const GemmArgs &p, int blocks, int omode, hipStream_t s) {
   dim3 grid((unsigned)blocks), block(WD_WAVES * WAVE);
-  if (pairs) hipLaunchKernelGGL((k_gemm_up_direct<true>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((k_gemm_up_direct<false>), grid, block, 0, s, p);
+  if (omode == 2) hipLaunchKernelGGL((k_gemm_up_direct<2>), grid, block, 0, s, p);
+  else if (omode == 1) hipLaunchKernelGGL((k_gemm_up_direct<1>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_gemm_up_direct<0>), grid, block, 0, s, p);
   return 0;
 }

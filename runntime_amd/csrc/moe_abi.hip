@@ -596,9 +596,19 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   // Both products on the grouped GEMM: act stays in dispatch order, so down
   // streams each tile's rows contiguously instead of gathering them; down
   // may split K in two partial products, which the combine adds.
+  // With f16 x (the direct-weight up GEMM) act goes between them as int8
+  // limbs and down runs on the int8 matrix cores, whole K (gemm_i8.hip).
+  size_t act_floats = (size_t)A * I;
   if (expert_uses_gemm(up) && expert_uses_gemm(dn)) {
     up.dispatch_order = dn.dispatch_order = 1;
-    dn.parts = gemm_down_parts(dn);
+    if (gemm_wide_eligible(up) && gemm_i8_down_eligible(dn)) {
+      up.act_i8 = dn.act_i8 = 1;
+      dn.parts = 1;
+      const size_t limb_floats = (size_t)((gemm_i8_act_bytes(A, E, I) + 3) / 4);
+      if (limb_floats > act_floats) act_floats = limb_floats;
+    } else {
+      dn.parts = gemm_down_parts(dn);
+    }
   } else {
     dn.parts = 1;
   }
@@ -614,7 +624,7 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
   // normalised copy xn.
   const bool stage_norm = norm && T <= FUSED_T && expert_stages_norm(up);
   if ((rc = plan_ws(ctx, calls, T, k, E, route_out ? 0 : (size_t)T * 2 * k,
-                    router_partial_floats(T, d, E), (size_t)A * I, (size_t)dn.parts * A * d, L,
+                    router_partial_floats(T, d, E), act_floats, (size_t)dn.parts * A * d, L,
                     norm ? (stage_norm ? (size_t)T * 4 : (size_t)T * d * esize) : 0, fixed)))
     return rc;
   hipStream_t s = ctx->stream;
@@ -1004,8 +1014,12 @@ extern "C" int moe_ctx_reserve_batched(moe_ctx *ctx, int calls, int T, int d, in
           "moe_ctx_reserve: sizes must be positive");
   LayerWs L;
   // y: room for down's two K parts (the grouped GEMM may split K).
+  // act: room for the int8-limb form over padded rows (gemm_i8.hip).
+  size_t act_floats = (size_t)T * k * I;
+  const size_t limb_floats = (size_t)((gemm_i8_act_bytes(T * k, E, I) + 3) / 4);
+  if (limb_floats > act_floats) act_floats = limb_floats;
   return plan_ws(ctx, calls, T, k, E, (size_t)T * 2 * k, router_partial_floats(T, d, E),
-                 (size_t)T * k * I, (size_t)2 * T * k * (d > I ? d : I), L);
+                 act_floats, (size_t)2 * T * k * (d > I ? d : I), L);
 }
 
 // ------------------------------------------------------------ weight upload

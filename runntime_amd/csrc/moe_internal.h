@@ -191,6 +191,10 @@ struct ExpertArgs {
   // Down on the grouped GEMM: K split into `parts` halves whose partial
   // products go to out + part·A·N (the combine adds them). 0 or 1 = whole K.
   int parts;
+  // Both products of the fused layer on the int8-limb act form: up (the
+  // f16-x grouped GEMM) writes act as int8 limbs over padded rows, down runs
+  // on the int8 matrix cores (gemm_i8.hip). Implies dispatch_order.
+  int act_i8;
   // Up of moe_block on the skinny kernel: x is normalised while staging,
   // row t scaled by a_inv[t] (written by the router) and the weight
   // a_normw [K] of x's dtype; NULL for plain x.
@@ -209,6 +213,12 @@ bool expert_stages_norm(const ExpertArgs &ea);
 // K parts the grouped GEMM uses for this down product (1 or 2): 2 when the
 // split evens out the last round of tiles over the CUs.
 int gemm_down_parts(const ExpertArgs &ea);
+// The int8-limb act form of the fused layer (gemm_i8.hip): whether down can
+// take it, and the bytes of act in that form.
+bool gemm_i8_down_eligible(const ExpertArgs &dn);
+// The direct-weight up GEMM (gemm_wide.hip) takes these arguments.
+bool gemm_wide_eligible(const ExpertArgs &ea);
+int64_t gemm_i8_act_bytes(int A, int E, int K);
 int launch_expert_gemm(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
 // Fills n floats with 0 (a kernel, not hipMemsetAsync, so a captured graph
 // replays it correctly).

@@ -30,6 +30,7 @@ class MoeConfig:
     zipf: float = 0.0  # Zipf exponent of the router bias, 0 = none
     hot_share: float = 0.20  # share of tokens routed to the hottest expert under zipf
     tokens: int = 0  # decode configs: independent single-token calls timed
+    empty: int = 0  # under zipf: the coldest `empty` experts get a bias no token overcomes
 
     @property
     def assignments(self) -> int:
@@ -42,7 +43,7 @@ CONFIGS = {
     3: MoeConfig("c3_decode_T8_d2048_E64_k8_I1408_f16", 8, 2048, 64, 8, 1408, "f16"),
     4: MoeConfig("c4_prefill_T4096_d2048_E32_k4_I5632_f16", 4096, 2048, 32, 4, 5632, "f16"),
     5: MoeConfig("c5_skewed_T4096_d2048_E128_k8_I1408_f16", 4096, 2048, 128, 8, 1408, "f16",
-                 zipf=1.2),
+                 zipf=1.2, empty=6),
 }
 
 
@@ -78,7 +79,8 @@ def _expert_weight(E, K, N, g, device, keep_q, bias_rand=False):
 def zipf_bias(cfg: MoeConfig, x: torch.Tensor, router_w: torch.Tensor, seed: int) -> torch.Tensor:
     """b_e = c·rank(e)^(−s) over a seeded permutation of the experts, with c
     chosen (bisection, f64 on the CPU) so that about `hot_share` of the
-    tokens route to the hottest expert.
+    tokens route to the hottest expert; the `empty` coldest experts (the
+    tail of the Zipf ranking) get −1e4 on top, so no token reaches them.
 
     The share is of tokens, not of the T·k assignments: a token picks an
     expert at most once, so one expert can hold at most 1/k of the
@@ -90,6 +92,12 @@ def zipf_bias(cfg: MoeConfig, x: torch.Tensor, router_w: torch.Tensor, seed: int
     rank[perm] = torch.arange(1, cfg.E + 1, dtype=torch.float64)
     shape = rank.pow(-cfg.zipf)
     logits = x.double().cpu() @ router_w.double().cpu()
+    # The Zipf tail's coldest experts: pushed far below every logit (the
+    # logits are O(1)), so they receive no tokens.
+    tail = torch.zeros(cfg.E, dtype=torch.float64)
+    if cfg.empty:
+        tail[rank > cfg.E - cfg.empty] = -1.0e4
+    logits = logits + tail
 
     def hottest(c):
         ids = torch.topk(logits + c * shape, cfg.k, dim=1).indices
@@ -105,7 +113,7 @@ def zipf_bias(cfg: MoeConfig, x: torch.Tensor, router_w: torch.Tensor, seed: int
         else:
             hi = mid
     c = float(np.float32(hi))
-    return (c * shape).float()
+    return (c * shape + tail).float()
 
 
 def make_inputs(cfg: MoeConfig, seed: int = 0, device="cuda", keep_q: bool = False,
