@@ -32,15 +32,23 @@
 // are whole lines, and its LDS image is the MFMA A fragments as they are
 // read (16 lanes read 256 contiguous bytes).
 //
-// Tiles: 64 rows (one act block) × 128 units (512 columns) per block of four
-// wavefronts, one per SIMD. Wavefront w takes all 64 rows and units
-// 32w .. 32w + 31: 2 row tiles × 4 column tiles × 3 limbs = 24 MFMAs and 384
-// i32 accumulators (in AGPRs and VGPRs). Lane l = 32hf + u holds unit u of
-// the wavefront for k half hf; per step it loads the unit's 64 contiguous
+// Tiles: 64 rows (one act block) × 128 units (512 columns) per block of
+// eight wavefronts, two per SIMD. Wavefront w takes rows 32·(w >> 2) ..
+// + 31 and units 32·(w & 3) .. + 31: 4 column tiles × 3 limbs = 12 MFMAs
+// per 32 k and 192 i32 accumulators, so two wavefronts fit a SIMD and each
+// hides the other's waits (one wavefront per SIMD with 64 rows × 32 units
+// needs 384 accumulators and measured 15-25% slower). Lane l = 32hf + u
+// holds unit u of the group for k half hf: per step it reads the unit's 64
 // bytes for its half (four quantW tiles of 4 columns × 4 k), and column c's
 // dwords of the four tiles are the B operand of column tile c (columns
-// 4u + c): no exchange between lanes. act comes through an LDS ring of step
-// pairs; the weights straight into registers, two steps ahead.
+// 4u + c): no exchange between lanes. act and the weights both come through
+// LDS rings of step pairs filled by direct-to-LDS loads of whole lines.
+//
+// Measured at config 4 (per launch, on one box): the loads alone (no
+// MFMAs) take 0.87 M cycles at 2.24 GHz, the MFMAs and LDS reads alone
+// 0.82 M cycles at 2.06 GHz, the kernel 1.1 M cycles at 1.81 GHz: under the
+// full load the clock drops (power), which is most of what separates the
+// kernel from its parts.
 //
 // Order of tiles: expert, then N-tile, then 64-row block, cut into 8
 // contiguous ranges, one per XCD (block b runs on XCD b mod 8), so the
@@ -48,20 +56,19 @@
 // of a row block — which share its act — run at once on one L2.
 #include "gemm_dev.h"
 
-#include <type_traits>
 
 namespace {
 
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int I8_WAVES = 4;
+constexpr int I8_WAVES = 8;
 constexpr int I8_BM = 64;                        // rows per tile (one act block)
 constexpr int I8_UNITS = 128;                    // weight units per tile
 constexpr int I8_SPA = 4;                        // act ring stages (step pairs)
 constexpr int I8_SPW = 3;                        // weight ring stages (step pairs)
 constexpr int I8_PAIR = I8_BM * 64 * 3;          // act bytes of one pair: 12 KB
-constexpr int I8_DMA = I8_PAIR / 1024 / I8_WAVES;  // act loads per wavefront and pair: 3
-constexpr int I8_WPAIR = I8_WAVES * 2 * 32 * 128;  // weights of one pair: 32 KB
+constexpr int I8_LOADS = 6;                      // loads per wavefront and pair (2 act, 4 weights)
+constexpr int I8_WPAIR = 4 * 2 * 32 * 128;        // weights of one pair: 32 KB
 constexpr int I8_MAX_E = GEMM_MAX_E;
 
 struct I8Args {
@@ -79,37 +86,15 @@ struct I8Args {
   int nt;                  // N-tiles (512 columns each)
 };
 
-// acc += A·B on the int8 matrix cores. Limbs h and m accumulate in AGPRs,
-// limb l in VGPRs: 384 accumulators do not fit the 256 VGPRs, and an asm
-// operand class keeps the register allocator from moving them between the
-// two files (with the builtin it spills and copies them). The compiler does
-// not see into the asm, so the hazards it would cover are covered here: the
-// B operand is assembled by VALU moves just before, and an MFMA may read a
-// VGPR a VALU instruction wrote only 2 wait states later (s_nop 2 gives 3);
-// the results are read only after drain_mfma().
-template <int L3>
-__device__ __forceinline__ void mfma_i8(i32x16 &acc, i32x4 a, i32x4 b, std::integral_constant<int, L3>) {
-  if constexpr (L3 < 2)
-    asm volatile("s_nop 2\n\tv_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-  else
-    asm volatile("s_nop 2\n\tv_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
-}
-
-// Wait states between the last MFMA and the first read of its result (a
-// 16-pass XDL result is readable 18 wait states after issue).
-__device__ __forceinline__ void drain_mfma() {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-}
-
 __device__ __forceinline__ int fresh_lane_i8() {
   int l;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
   return l;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_gemm_down_i8(I8Args p) {
-  __shared__ __align__(16) uint8_t aring[I8_SPA * I8_PAIR];  // 48 KB
+  __shared__ __align__(16) uint8_t aring[I8_SPA * I8_PAIR];   // 48 KB
   __shared__ __align__(16) uint8_t wring[I8_SPW * I8_WPAIR];  // 96 KB
   __shared__ __align__(16) uint8_t junk[1024];
   __shared__ int32_t rowmap[I8_BM];
@@ -145,21 +130,22 @@ void k_gemm_down_i8(I8Args p) {
 
   const int lane = tid & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+  const int rg = wave >> 2, cg = wave & 3;  // row half, unit group of the wavefront
   const int hf = lane >> 5, u = lane & 31;
   const int N4 = p.N / 4;
   const int ksteps = p.K / BK, npairs = ksteps / 2;
   const uint64_t slab = (uint64_t)p.K * (uint64_t)p.N;
   const i32x4 ar = buffer_rsrc(p.act, p.act_bytes);
   const uint32_t aring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)aring;
-  const uint32_t junk0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)junk;
   const uint32_t wring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)wring;
+  const uint32_t junk0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)junk;
   const __amdgpu_buffer_rsrc_t yrc = __builtin_amdgcn_make_buffer_rsrc(p.y, 0, p.y_bytes, BUF_DWORD3);
+  const int swu = sw8(u);
 
   for (int L = start; L < end; L += bx) {
     // ---- the tile: expert (binary search over the block counts), N-tile,
-    // row block.
+    // row block. Tiles of active expert i: c64[i]·nt .. c64[i + 1]·nt.
     int lo = 0, hi = n_active - 1;
-    // Tiles of active expert i: c64[i]·nt .. c64[i + 1]·nt.
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (c64[mid] * p.nt <= L) lo = mid; else hi = mid - 1;
@@ -176,31 +162,18 @@ void k_gemm_down_i8(I8Args p) {
 
     if (tid < I8_BM) rowmap[tid] = p.perm[r0 + min(tid, rows - 1)];
 
-    // act pair j of this block: 12 chunks of 1 KB; wavefront w loads chunks
-    // 3w .. 3w + 2, lane l bytes 16l of each (whole lines).
+    // Loads of a pair, 6 per wavefront: act chunks 2w, 2w + 1 (12 chunks of
+    // 1 KB over wavefronts 0-5; wavefronts 6 and 7 load into the junk area
+    // so that every wavefront issues the same count), then the weights of
+    // step rg of the pair for units 32·cg .. 32·cg + 31: instruction i loads
+    // units 8i .. 8i + 7 of the group, lane l the 16-byte chunk
+    // (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes, so that chunk c
+    // of unit u sits at u·128 + (c ^ sw8(u))·16 (the 16 lanes reading one
+    // tile of 16 units hit 16 different bank groups). A unit past N reads
+    // the last unit (its outputs are not stored). Past the last pair every
+    // load goes to the junk area. Branch-free: a load under a branch makes
+    // the compiler wait for every load in flight where the paths join.
     const uint32_t a_base = (uint32_t)blk * (uint32_t)npairs * (uint32_t)I8_PAIR;
-    auto issue_a = [&](int j, int stage) {
-      const int ln = fresh_lane_i8();
-#pragma unroll
-      for (int i = 0; i < I8_DMA; i++) {
-        const int c = I8_DMA * wave + i;
-        dma16(ar, a_base + (uint32_t)j * I8_PAIR + (uint32_t)c * 1024u + (uint32_t)ln * 16u, 0,
-              aring0 + stage * I8_PAIR + c * 1024);
-      }
-    };
-    // Placeholder loads (into a junk LDS area) keep the per-pair count of
-    // vector memory instructions constant in the prologue and past the end.
-    auto issue_junk = [&](int n) {
-      for (int i = 0; i < n; i++) dma16(ar, 0u, 0, junk0);
-    };
-    // Weights of pair j (steps 2j, 2j + 1) for wavefront w's 32 units, by
-    // direct-to-LDS loads of whole lines: instruction (q, i) loads units
-    // 8i .. 8i + 7 of the wavefront, lane l the 16-byte chunk
-    // (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes of step 2j + q,
-    // so that chunk c of unit u sits at u·128 + (c ^ sw8(u))·16: the 16
-    // lanes reading one tile of 16 units hit 16 different bank groups. A unit
-    // past N reads the last unit (its outputs are not stored).
-    const int unit_last = N4 - 1;
     const i32x4 wr = buffer_rsrc(p.w + (uint64_t)e * slab, (uint32_t)slab);
     uint32_t woff[4];
     {
@@ -208,160 +181,122 @@ void k_gemm_down_i8(I8Args p) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int uu = 8 * i + (ln >> 3);
-        const int ug = min(U0 + 32 * wave + uu, unit_last);
+        const int ug = min(U0 + 32 * cg + uu, N4 - 1);
         woff[i] = (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u;
       }
     }
-    auto issue_w = [&](int j, int stage) {
+    auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
+      if (n < 2) {
+        const int c = 2 * wave + n;
+        const bool ok = ja < npairs && c < 12;
+        const uint32_t at = a_base + (uint32_t)ja * I8_PAIR + (uint32_t)c * 1024u +
+                            (uint32_t)fresh_lane_i8() * 16u;
+        dma16(ar, ok ? at : 0u, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
+      } else {
+        const int i = n - 2;
+        const bool ok = jw >= 0 && jw < npairs;
+        dma16(wr, woff[i], ok ? (2 * jw + rg) * (BK * 4) : 0,
+              ok ? wring0 + sw_ * I8_WPAIR + cg * 8192 + rg * 4096 + i * 1024 : junk0);
+      }
+    };
+    auto issue_pair = [&](int ja, int sa_, int jw, int sw_) {
 #pragma unroll
-      for (int q = 0; q < 2; q++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          dma16(wr, woff[i], (2 * j + q) * (BK * 4),
-                wring0 + stage * I8_WPAIR + wave * 8192 + q * 4096 + i * 1024);
+      for (int n = 0; n < I8_LOADS; n++) issue_one(n, ja, sa_, jw, sw_);
     };
 
-    i32x16 acc[2][4][3];
+    i32x16 acc[4][3];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int c = 0; c < 4; c++)
 #pragma unroll
-      for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int l3 = 0; l3 < 3; l3++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) acc[i][c][l3][r] = 0;
+      for (int l3 = 0; l3 < 3; l3++) acc[c][l3] = i32x16{};
 
-    // The pipeline. Frags of a step are read from LDS during the previous
-    // step's MFMAs. In the middle of pair j (between its two steps) every
-    // wavefront waits for pair j + 1's loads and a barrier follows: then all
-    // of pair j's LDS has been read, so the act loads of pair j + SPA and the
-    // weight loads of pair j + SPW go into pair j's stages (3 + 8 per
-    // wavefront, 11 vector memory instructions per pair), and pair j + 1's
-    // first frags are read. At the wait, pair j + 1's weights (issued one
-    // pair after its act) are followed by exactly one pair's 11 younger
-    // instructions. The prologue issues virtual pairs −SPA .. −1 of the same
-    // pattern (placeholders where a pair is out of range).
+    // The pipeline: after the barrier of pair j (its loads landed, every
+    // read of pair j − 1 done), the act loads of pair j + SPA − 1 and the
+    // weight loads of pair j + SPW − 1 go into pair j − 1's stages, spread
+    // between the MFMA groups of step 2j (all wavefronts issuing them in one
+    // burst stalls the matrix cores together). At the wait of pair j, its
+    // weights (issued one pair after its act) are followed by exactly one
+    // pair's I8_LOADS younger instructions. The prologue issues virtual
+    // pairs −(SPA − 1) .. −1 of the same pattern.
     static_assert(I8_SPA == I8_SPW + 1, "act runs one pair ahead of the weights");
 #pragma unroll
-    for (int v = 0; v < I8_SPA; v++) {
-      if (v < npairs) issue_a(v, v);
-      else issue_junk(I8_DMA);
-      const int jw = v - 1;
-      if (jw >= 0 && jw < npairs) issue_w(jw, jw);
-      else issue_junk(8);
-    }
+    for (int v = 0; v < I8_SPA - 1; v++) issue_pair(v, v, v - 1, v - 1);
 
-    // Fragments of step q of the pair in LDS stages sa (act), sw (weights):
-    // act of row tile rt, limb l3 for half hf; the weight unit's four tiles
-    // for half hf (tile t = column 0..3 × k 4t .. 4t + 3).
+    // Fragments of step q of the pair: act rows 32·rg + u, limb l3, half hf;
+    // the unit's four quantW tiles for half hf (tile t = columns 0..3 × k
+    // 4t .. 4t + 3).
     struct Frags {
-      u32x4 a[2][3];
+      u32x4 a[3];
       u32x4 w[4];
     };
-    const int swu = sw8(u);
     auto read_frags = [&](Frags &F, int sa, int sw, int q) {
-      const uint8_t *s = aring + sa * I8_PAIR + hf * 1024 + u * 16 + q * 2048;
+      const uint8_t *s = aring + sa * I8_PAIR + hf * 1024 + (32 * rg + u) * 16 + q * 2048;
 #pragma unroll
-      for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-        for (int l3 = 0; l3 < 3; l3++) F.a[rt][l3] = *(const u32x4 *)(s + l3 * 4096 + rt * 512);
-      const uint8_t *t = wring + sw * I8_WPAIR + wave * 8192 + q * 4096 + u * 128;
+      for (int l3 = 0; l3 < 3; l3++) F.a[l3] = *(const u32x4 *)(s + l3 * 4096);
+      const uint8_t *t = wring + sw * I8_WPAIR + cg * 8192 + q * 4096 + u * 128;
 #pragma unroll
       for (int j4 = 0; j4 < 4; j4++) F.w[j4] = *(const u32x4 *)(t + ((hf * 4 + j4) ^ swu) * 16);
     };
-    // MFMAs of one step; hook(slot) runs after each of the 8 groups of three.
+    // The 12 MFMAs of a step; hook(c) runs after column tile c's three.
     auto mfmas = [&](const Frags &F, auto hook) {
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         // Column c's dwords of the four quantW tiles: 16 k of column 4u + c.
         const i32x4 B = {(int)F.w[0][c], (int)F.w[1][c], (int)F.w[2][c], (int)F.w[3][c]};
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) {
-          mfma_i8(acc[rt][c][0], __builtin_bit_cast(i32x4, F.a[rt][0]), B, std::integral_constant<int, 0>());
-          mfma_i8(acc[rt][c][1], __builtin_bit_cast(i32x4, F.a[rt][1]), B, std::integral_constant<int, 1>());
-          mfma_i8(acc[rt][c][2], __builtin_bit_cast(i32x4, F.a[rt][2]), B, std::integral_constant<int, 2>());
-          hook(2 * c + rt);
-        }
-      }
-    };
-    auto no_hook = [](int) {};
-    // Load number n (0..10) of a pair's 11: act chunks 0-2, then the weight
-    // instructions (q, i) in order. Branch-free: past the last pair the
-    // load goes to the junk area (a load under a branch makes the compiler
-    // wait for every load in flight where the paths join).
-    auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
-      if (n < I8_DMA) {
-        const bool ok = ja < npairs;
-        const int c = I8_DMA * wave + n;
-        const uint32_t at = a_base + (uint32_t)ja * I8_PAIR + (uint32_t)c * 1024u +
-                            (uint32_t)fresh_lane_i8() * 16u;
-        const uint32_t voff = ok ? at : 0u;
-        dma16(ar, voff, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
-      } else {
-        const bool ok = jw < npairs;
-        const int t = n - I8_DMA, q = t >> 2, i = t & 3;
-        dma16(wr, woff[i], ok ? (2 * jw + q) * (BK * 4) : 0,
-              ok ? wring0 + sw_ * I8_WPAIR + wave * 8192 + q * 4096 + i * 1024 : junk0);
+        for (int l3 = 0; l3 < 3; l3++)
+          acc[c][l3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, F.a[l3]), B,
+                                                             acc[c][l3], 0, 0, 0);
+        hook(c);
       }
     };
 
-    // Pair 0's loads: its weights are followed by two virtual pairs' 22.
-    WAIT_VMCNT(2 * (I8_DMA + 8));
-    block_barrier();
-    Frags Fa, Fb;
-    read_frags(Fa, 0, 0, 0);
     int sa = 0, sw = 0;
     for (int j = 0; j < npairs; j++) {
-      read_frags(Fb, sa, sw, 1);
-      mfmas(Fa, no_hook);
-      WAIT_VMCNT(I8_DMA + 8);
+      WAIT_VMCNT(I8_LOADS);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       block_barrier();
-      // This pair's stages are free: the loads of pairs j + SPA (act) and
-      // j + SPW (weights) go there, spread between the MFMA groups of the
-      // step below (all wavefronts issuing them in one burst stalls the
-      // matrix cores of the CU together).
-      const int ja = j + I8_SPA, jw = j + I8_SPW, sa0 = sa, sw0 = sw;
+      const int ja = j + I8_SPA - 1, jw = j + I8_SPW - 1;
+      const int na = sa == 0 ? I8_SPA - 1 : sa - 1, nw = sw == 0 ? I8_SPW - 1 : sw - 1;
+      Frags F;
+      read_frags(F, sa, sw, 0);
+      mfmas(F, [&](int c) {
+        issue_one(c, ja, na, jw, nw);
+        if (c < 2) issue_one(c + 4, ja, na, jw, nw);
+      });
+      read_frags(F, sa, sw, 1);
+      mfmas(F, [](int) {});
       sa = sa + 1 == I8_SPA ? 0 : sa + 1;
       sw = sw + 1 == I8_SPW ? 0 : sw + 1;
-      // (past the last pair this reads a stage that holds no pair: unused)
-      read_frags(Fa, sa, sw, 0);
-      mfmas(Fb, [&](int slot) {
-        issue_one(slot, ja, sa0, jw, sw0);
-        if (slot < 3) issue_one(slot + 8, ja, sa0, jw, sw0);
-      });
     }
     WAIT_VMCNT(0);
-    drain_mfma();
     block_barrier();
 
     // ---- epilogue: y[assignment][col .. col + 3] = scale · V-sum · 2^-17
     // + bias, for columns 4·unit' + 0..3 of the lane.
-    const int uo = U0 + 32 * wave + u;
+    const int uo = U0 + 32 * cg + u;
     const bool col_ok = uo < N4;
     const int col = 4 * min(uo, N4 - 1);
     const floatx4 sc = *(const floatx4 *)(p.scales + (size_t)e * p.N + col) * (1.0f / 131072.0f);
     floatx4 bs = {0.f, 0.f, 0.f, 0.f};
     if (p.bias) bs = *(const floatx4 *)(p.bias + (size_t)e * p.N + col);
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int r = 0; r < 16; r++) {
+      const int row = 32 * rg + 8 * (r / 4) + 4 * hf + (r % 4);
+      floatx4 o;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = 32 * rt + 8 * (r / 4) + 4 * hf + (r % 4);
-        floatx4 o;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          float v = (float)acc[rt][c][0][r] * 65536.0f;
-          v = __builtin_fmaf((float)acc[rt][c][1][r], 256.0f, v);
-          v += (float)acc[rt][c][2][r];
-          o[c] = __builtin_fmaf(v, sc[c], bs[c]);
-        }
-        const uint32_t off = (row < rows && col_ok)
-                                 ? ((uint32_t)rowmap[row] * (uint32_t)p.N + (uint32_t)col) * 4u
-                                 : 0x80000000u;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), yrc, off, 0, 0);
+      for (int c = 0; c < 4; c++) {
+        float v = (float)acc[c][0][r] * 65536.0f;
+        v = __builtin_fmaf((float)acc[c][1][r], 256.0f, v);
+        v += (float)acc[c][2][r];
+        o[c] = __builtin_fmaf(v, sc[c], bs[c]);
       }
-    // rowmap is rewritten by the next tile.
+      const uint32_t off = (row < rows && col_ok)
+                               ? ((uint32_t)rowmap[row] * (uint32_t)p.N + (uint32_t)col) * 4u
+                               : 0x80000000u;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), yrc, off, 0, 0);
+    }
+    // rowmap and the stages are rewritten by the next tile.
     block_barrier();
   }
 }
