@@ -121,6 +121,8 @@ def cpu_baseline(cfg, seconds_budget=15.0):
         i += 1
     dt = time.perf_counter() - t0
     return {"value": tokens / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "label": "restatement of the reference kernels, not the reference (the reference's "
+                     "WGSL path needs Node >= 22, TypeGPU and Dawn, none of which this image has)",
             "sample": f"{tokens} tokens of {cfg.name} in {step_T}-token calls, {dt:.1f} s; "
                       "oracle/moe_oracle.c f32 restatement of topkSelect/moeUp/moeDown "
                       "(32-lane K split, fixed tree merge), OpenMP over rows"}

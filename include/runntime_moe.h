@@ -189,9 +189,12 @@ MOE_API int moe_layer(moe_ctx *ctx, const void *x, moe_dtype x_dtype, const floa
  * ends, instead of the context's growable one; the call allocates nothing
  * and creates no timing events. A shape whose workspace exceeds it is
  * INVALID_ARGUMENT with the size it needs (decode-sized calls fit: T·k of a
- * few hundred rows). Every call on a GPU shares that GPU's array: calls that
- * overlap on one GPU (different streams or contexts without ordering)
- * race. */
+ * few hundred rows). Every call on a GPU shares that GPU's array. The
+ * library records which context and stream used it last: a call from
+ * another context or stream while that stream still has work queued is
+ * INVALID_ARGUMENT (synchronise the other stream first). What the record
+ * cannot see still races: work captured into a graph on another stream and
+ * replayed later, and calls from two host threads at once. */
 #define MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
 MOE_API int moe_layer_noalloc(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
                               const float *w_router, const float *b_router,

@@ -96,24 +96,74 @@ extern "C" int moe_prof_read(moe_ctx *ctx, int reset, double *ms_out, int64_t *c
 static __device__ __align__(256) char scratch[MOE_NOALLOC_SCRATCH_BYTES];
 constexpr int SCRATCH_MAX_DEVICES = 64;
 static char *g_scratch_ptr[SCRATCH_MAX_DEVICES];
-static hipError_t g_scratch_err[SCRATCH_MAX_DEVICES];
+// The last (context, stream) that used a device's scratch. A call from
+// another context or stream while that stream still has work queued would
+// race on the scratch; moe_layer_noalloc refuses it.
+struct ScratchOwner {
+  const moe_ctx *ctx;
+  hipStream_t stream;
+};
+static ScratchOwner g_scratch_owner[SCRATCH_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
 // The scratch address on `device` (current); NULL and an error if unknown.
+// A failed lookup is not remembered: the next call tries again.
 static char *scratch_on(int device, hipError_t *err) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (device < 0 || device >= SCRATCH_MAX_DEVICES) {
     *err = hipErrorInvalidDevice;
     return nullptr;
   }
-  if (!g_scratch_ptr[device] && g_scratch_err[device] == hipSuccess) {
+  *err = hipSuccess;
+  if (!g_scratch_ptr[device]) {
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) g_scratch_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
-    else g_scratch_ptr[device] = (char *)p;
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    g_scratch_ptr[device] = (char *)p;
   }
-  *err = g_scratch_err[device];
   return g_scratch_ptr[device];
+}
+
+// Claims `device`'s scratch for (ctx, ctx->stream): refused (false, with the
+// reason in *why) while another context or stream that used it last still
+// has work queued. Calls on one stream are ordered by the stream itself.
+static bool scratch_claim(const moe_ctx *ctx, std::string *why) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchOwner &o = g_scratch_owner[ctx->device];
+  // Under a stream capture nothing runs now (and querying other streams is
+  // not allowed while capturing): the record only moves to the capturing
+  // stream.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cap) != hipSuccess) {
+    (void)hipGetLastError();
+    cap = hipStreamCaptureStatusNone;
+  }
+  if (cap == hipStreamCaptureStatusNone && o.ctx && (o.ctx != ctx || o.stream != ctx->stream)) {
+    const hipError_t q = hipStreamQuery(o.stream);
+    (void)hipGetLastError();  // a not-ready query must not reach the next error check
+    if (q == hipErrorNotReady || q == hipErrorStreamCaptureUnsupported ||
+        q == hipErrorStreamCaptureInvalidated) {
+      *why = std::string(o.ctx != ctx ? "another context" : "another stream of this context") +
+             " used the static scratch of device " + std::to_string(ctx->device) +
+             " last and its stream has not finished: synchronise it first (calls that overlap "
+             "on one GPU would share the scratch)";
+      return false;
+    }
+  }
+  o.ctx = ctx;
+  o.stream = ctx->stream;
+  return true;
+}
+
+// A destroyed context no longer owns any scratch.
+static void scratch_release(const moe_ctx *ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  for (auto &o : g_scratch_owner)
+    if (o.ctx == ctx) o = ScratchOwner{};
 }
 
 extern "C" int moe_ctx_create(int device, void *stream, moe_ctx **out) {
@@ -226,6 +276,7 @@ extern "C" int moe_ctx_destroy(moe_ctx *ctx) {
   }
   for (auto e : ctx->prof_free) (void)hipEventDestroy(e);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  scratch_release(ctx);
   ctx->disposed = true;
   delete ctx;
   return MOE_OK;
@@ -702,6 +753,8 @@ extern "C" int moe_layer_noalloc(moe_ctx *ctx, const void *x, moe_dtype x_dtype,
     return moe_fail(MOE_EXECUTION_FAILED, std::string("moe_layer_noalloc: no scratch address on "
                                                       "device ") + std::to_string(ctx->device) +
                                               ": " + hipGetErrorString(e));
+  std::string why;
+  if (!scratch_claim(ctx, &why)) return moe_fail(MOE_INVALID_ARGUMENT, "moe_layer_noalloc: " + why);
   FixedWs fixed;
   fixed.base = base;
   fixed.size = MOE_NOALLOC_SCRATCH_BYTES;

@@ -1,6 +1,6 @@
 // Top-k gating of one token by one wavefront, shared by the router kernels
-// (router.hip) and the fused small-call layer (decode.hip), which must pick
-// the same ids and gates bit for bit.
+// of router.hip (the chunk fold with and without the fused dispatch, and the
+// standalone topk), which must pick the same ids and gates bit for bit.
 //
 // Reference: src/core/kernels/reduce/topkSelect.ts:21-92 (selection) and
 // :142-156 (softmax over the selected logits). Each lane owns experts lane,

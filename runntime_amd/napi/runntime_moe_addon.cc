@@ -95,6 +95,10 @@ struct Args {
       int64_t x = 0;
       bool lossless = false;
       napi_get_value_bigint_int64(env, v[i], &x, &lossless);
+      if (!lossless) {
+        fail("argument " + std::to_string(i) + ": integer out of int64 range");
+        return 0;
+      }
       return x;
     }
     double d = 0;
@@ -158,11 +162,23 @@ struct Args {
       fail("argument " + std::to_string(i) + ": expected a ValueMeta {elems, dtype, dims?}");
       return d;
     }
+    // elems and every dim must be non-negative integers, rank at most 4: a
+    // malformed meta must not reach the shape checks as another, valid-looking
+    // shape.
+    auto whole = [&](napi_value y, int64_t *out) {
+      double dv = 0;
+      if (napi_get_value_double(env, y, &dv) != napi_ok || !(dv >= 0) || dv > 9.0e15 ||
+          dv != (double)(int64_t)dv)
+        return false;
+      *out = (int64_t)dv;
+      return true;
+    };
     napi_value x;
-    double e = 0;
     napi_get_named_property(env, v[i], "elems", &x);
-    napi_get_value_double(env, x, &e);
-    d.elems = (int64_t)e;
+    if (!whole(x, &d.elems)) {
+      fail("argument " + std::to_string(i) + ": ValueMeta.elems must be a non-negative integer");
+      return d;
+    }
     napi_get_named_property(env, v[i], "dtype", &x);
     char dt[16] = {0};
     size_t n = 0;
@@ -175,16 +191,25 @@ struct Args {
       napi_get_named_property(env, v[i], "dims", &x);
       bool arr = false;
       napi_is_array(env, x, &arr);
-      if (arr) {
-        uint32_t len = 0;
-        napi_get_array_length(env, x, &len);
-        d.rank = len > 4 ? 4 : (int)len;
-        for (uint32_t k = 0; k < (uint32_t)d.rank; k++) {
-          napi_value el;
-          double dv = 0;
-          napi_get_element(env, x, k, &el);
-          napi_get_value_double(env, el, &dv);
-          d.dims[k] = (int64_t)dv;
+      if (!arr) {
+        fail("argument " + std::to_string(i) + ": ValueMeta.dims must be an array");
+        return d;
+      }
+      uint32_t len = 0;
+      napi_get_array_length(env, x, &len);
+      if (len > 4) {
+        fail("argument " + std::to_string(i) + ": ValueMeta.dims has rank " + std::to_string(len) +
+             "; at most 4 is supported");
+        return d;
+      }
+      d.rank = (int)len;
+      for (uint32_t k = 0; k < len; k++) {
+        napi_value el;
+        napi_get_element(env, x, k, &el);
+        if (!whole(el, &d.dims[k])) {
+          fail("argument " + std::to_string(i) + ": ValueMeta.dims[" + std::to_string(k) +
+               "] must be a non-negative integer");
+          return d;
         }
       }
     }

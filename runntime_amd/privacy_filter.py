@@ -265,31 +265,19 @@ class ViterbiBiases:
     end_to_start: float = 0.0
 
 
-# The decoder's moves, as a table: (group of the previous label, role of the
-# next label) → the ViterbiBiases field added to an allowed move (None: 0).
-# Roles: "O" background (its span class is the background one, or it is the
-# background token), "B"/"I"/"E"/"S" a boundary tag of a span class, "X" a
-# label without a span class or without a tag, "Z" a span class with a tag
-# other than B/I/E/S. Groups of the previous label: "O"; "BI" (inside a span:
-# only I or E of the same span class may follow); "ES" (a span just ended);
-# "X" (may start anything, with no bias); "Z" (nothing may follow). Any pair
-# not listed, and any next label of role "X" or "Z", is not allowed.
-_MOVES = {
-    ("O", "O"): "background_stay", ("O", "B"): "background_to_start",
-    ("O", "S"): "background_to_start",
-    ("ES", "O"): "end_to_background", ("ES", "B"): "end_to_start", ("ES", "S"): "end_to_start",
-    ("X", "O"): None, ("X", "B"): None, ("X", "S"): None,
-    ("BI", "I"): "inside_to_continue", ("BI", "E"): "inside_to_end",
-}
-_GROUP = {"O": "O", "B": "BI", "I": "BI", "E": "ES", "S": "ES", "X": "X", "Z": "Z"}
-
-
 class ViterbiDecoder:
     """The constrained BIOES decoder (viterbi.ts:20-148): start/end scores
     and a transition matrix of allowed moves (−1e9 elsewhere) with the
-    optional biases; ties keep the lower previous label. The allowed moves
-    and their biases are the table above; the reference states the same
-    rules as nested conditions (viterbi.ts:20-82)."""
+    optional biases; ties keep the lower previous label.
+
+    The rules (viterbi.ts:39-77) are the BIOES semantics, so they are stated
+    as the reference states them: a label is background when its span class
+    is the background one or it is the background token. A next label that
+    is neither background nor a tagged span label is never allowed. After a
+    label with no span class or no tag, after background, and after an E or
+    S tag, only background, B or S may follow; after B or I only I or E of
+    the same span class. The bias of an allowed move is looked up on the
+    previous label's background status first, then on its tag."""
     NEG_INF = -1e9
 
     def __init__(self, info: LabelInfo, biases: Optional[ViterbiBiases] = None):
@@ -297,31 +285,43 @@ class ViterbiDecoder:
         n = info.num_classes
         self.n = n
         cls = [info.token_to_span_label.get(i) for i in range(n)]
-
         tags = [info.token_boundary_tags.get(i) for i in range(n)]
-
-        def role(i):
-            if cls[i] == info.background_span_label or i == info.background_token_label:
-                return "O"
-            if cls[i] is None or tags[i] is None:
-                return "X"
-            return tags[i] if tags[i] in ("B", "I", "E", "S") else "Z"
-
-        roles = [role(i) for i in range(n)]
         bg = info.background_token_label
-        starts = {i for i in range(n) if tags[i] in ("B", "S") or i == bg}
-        ends = {i for i in range(n) if tags[i] in ("E", "S") or i == bg}
-        self.start = np.array([0.0 if i in starts else self.NEG_INF for i in range(n)])
-        self.end = np.array([0.0 if i in ends else self.NEG_INF for i in range(n)])
+        is_bg = [cls[i] == info.background_span_label or i == bg for i in range(n)]
+        opens = [is_bg[i] or tags[i] in ("B", "S") for i in range(n)]  # may follow a closed span
+
+        def allowed(p, q):
+            if not is_bg[q] and (cls[q] is None or tags[q] is None):
+                return False
+            if cls[p] is None or tags[p] is None or is_bg[p] or tags[p] in ("E", "S"):
+                return opens[q]
+            if tags[p] in ("B", "I"):
+                return cls[p] == cls[q] and tags[q] in ("I", "E")
+            return False
+
+        def move_bias(p, q):
+            if is_bg[p]:
+                return (b.background_stay if is_bg[q] else
+                        b.background_to_start if tags[q] in ("B", "S") else 0.0)
+            if tags[p] in ("B", "I"):
+                if cls[p] != cls[q]:
+                    return 0.0
+                return (b.inside_to_continue if tags[q] == "I" else
+                        b.inside_to_end if tags[q] == "E" else 0.0)
+            if tags[p] in ("E", "S"):
+                return (b.end_to_background if is_bg[q] else
+                        b.end_to_start if tags[q] in ("B", "S") else 0.0)
+            return 0.0
+
+        self.start = np.array([0.0 if tags[i] in ("B", "S") or i == bg else self.NEG_INF
+                               for i in range(n)])
+        self.end = np.array([0.0 if tags[i] in ("E", "S") or i == bg else self.NEG_INF
+                             for i in range(n)])
         self.trans = np.full((n, n), self.NEG_INF, dtype=np.float64)
         for p in range(n):
-            g = _GROUP[roles[p]]
             for q in range(n):
-                key = (g, roles[q])
-                if key not in _MOVES or (g == "BI" and cls[p] != cls[q]):
-                    continue
-                field = _MOVES[key]
-                self.trans[p, q] = getattr(b, field) if field else 0.0
+                if allowed(p, q):
+                    self.trans[p, q] = move_bias(p, q)
 
     def decode(self, log_probs: np.ndarray) -> List[int]:
         """The library's native decode (moe_viterbi_decode): ties keep the

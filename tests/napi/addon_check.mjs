@@ -40,4 +40,12 @@ for (const [name, over] of cases) {
   const c = Object.assign({}, base, over);
   res.checks.push([name, caught(() => addon.checkExpertWeight('moeUp', c.w, c.scales, c.bias, c.route, 8, 3, 4, c.bits, c.g))]);
 }
+// Malformed ValueMeta and integers past int64 are refused before any shape
+// check runs.
+res.malformed = [
+  ['rank 5', caught(() => addon.checkExpertWeight('moeUp', { elems: 64, dtype: 'quantW', dims: [16, 16, 1, 1, 1] }, base.scales, base.bias, base.route, 8, 3, 4, 8, 4))],
+  ['fractional dim', caught(() => addon.checkExpertWeight('moeUp', { elems: 64, dtype: 'quantW', dims: [16.5, 16] }, base.scales, base.bias, base.route, 8, 3, 4, 8, 4))],
+  ['string elems', caught(() => addon.checkExpertWeight('moeUp', { elems: '64', dtype: 'quantW', dims: [16, 16] }, base.scales, base.bias, base.route, 8, 3, 4, 8, 4))],
+  ['int64 overflow', caught(() => addon.checkExpertWeight('moeUp', base.w, base.scales, base.bias, base.route, 2n ** 70n, 3, 4, 8, 4))],
+];
 console.log(JSON.stringify(res));

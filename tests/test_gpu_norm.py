@@ -15,6 +15,7 @@ import runntime_amd as rt
 from oracle import ref
 from runntime_amd.synth import CONFIGS, make_inputs
 from tests.helpers import assert_close
+from tests.test_gpu_parity import _edge_tokens
 from tests.test_oracle_norm import OPTIONS, SHAPES, inputs
 
 pytestmark = pytest.mark.gpu
@@ -102,7 +103,7 @@ def _oracle_block(inp, norm_w, eps, tokens):
     return route, out
 
 
-@pytest.mark.parametrize("cid,sample", [(1, None), (2, None), (3, None), (4, 6)])
+@pytest.mark.parametrize("cid,sample", [(1, None), (2, None), (3, None), (4, 256), (5, 256)])
 def test_moe_block_matches_oracle(cid, sample):
     cfg = CONFIGS[cid]
     say(f"moe_block config {cid}: {cfg.name}")
@@ -111,7 +112,14 @@ def test_moe_block_matches_oracle(cid, sample):
     out, route = rt.moe_block(inp.x, nw, 1e-5, inp.router_w, inp.router_b, inp.glu, inp.lin,
                               inp.down, cfg.k, return_route=True)
     got_out, got_route = host(out), host(route)
-    tokens = np.arange(cfg.T) if sample is None else np.linspace(0, cfg.T - 1, sample).astype(int)
+    if sample is None:
+        tokens = np.arange(cfg.T)
+    else:
+        # an even spread plus every token at a row-tile edge of the grouped
+        # GEMMs (the prefill path normalises into a copy before them)
+        edge = _edge_tokens(got_route[:, :cfg.k], cfg.E, cfg.k)
+        tokens = np.array(sorted(set(np.linspace(0, cfg.T - 1, sample).astype(int).tolist()) | edge))
+        say(f"  checking {len(tokens)} of {cfg.T} tokens ({len(edge)} at tile edges)")
     want_route, want_out = _oracle_block(inp, nw, 1e-5, tokens)
     k = cfg.k
     assert np.array_equal(got_route[tokens, :k], want_route[:, :k]), "expert ids differ"
@@ -123,10 +131,12 @@ def test_moe_block_matches_oracle(cid, sample):
                                            (2, 100, "f16"), (2, 40, "f16"), (4, None, None)])
 def test_moe_block_is_norm_then_layer(cid, T, x_dtype):
     """moe_block = rmsNorm → moe_layer(xn) with residual x, bit for bit.
-    The block normalises x while staging it where the gate/up product runs on
-    the skinny kernel (configs 1-3 and the T = 40 / 100 cases: the fused and
-    the register-tiled router) and through a normalised copy for the grouped
-    GEMM (config 4)."""
+    The block normalises x while staging it for calls of at most 64 tokens
+    whose gate/up product runs on the skinny kernel (configs 1-3 and T = 40:
+    the fused router); above 64 tokens it writes a normalised copy first,
+    for the register-tiled router (T = 100, whose staged-norm branch is
+    refused by the router and so must not be reached: this case passing
+    shows the copy path ran) and for the grouped GEMM (config 4)."""
     import dataclasses
     cfg = CONFIGS[cid]
     if T:

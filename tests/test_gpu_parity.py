@@ -318,10 +318,11 @@ def _oracle_layer(inp, tokens):
     return route, out, logits
 
 
-def _edge_tokens(ids, E, k, tile=128):
-    """Tokens whose assignments sit at the edges of the grouped GEMM's row
-    tiles: each active expert's first two rows, the first two and last two
-    rows of its last 128-row tile, and every row of the hottest expert's last
+def _edge_tokens(ids, E, k, tiles=(128, 64)):
+    """Tokens whose assignments sit at the edges of the grouped GEMMs' row
+    tiles (128 rows for gate/up, 64 for the int8 down GEMM): each active
+    expert's first two rows, the first two and last two rows of its last
+    tile of each size, and every row of the hottest expert's last 128-row
     tile (rows in the dispatch's stable order by expert)."""
     flat = ids.astype(np.int64).ravel()
     order = np.argsort(flat, kind="stable")
@@ -333,10 +334,12 @@ def _edge_tokens(ids, E, k, tile=128):
         if n == 0:
             continue
         rows = order[start:start + n]
-        last = (n - 1) // tile * tile
-        pick = list(rows[:2]) + list(rows[last:last + 2]) + list(rows[-2:])
-        if e == hot:
-            pick += list(rows[last:])
+        pick = list(rows[:2]) + list(rows[-2:])
+        for tile in tiles:
+            last = (n - 1) // tile * tile
+            pick += list(rows[last:last + 2])
+            if e == hot and tile == tiles[0]:
+                pick += list(rows[last:])
         toks.update(int(a) // k for a in pick)
         start += n
     return toks

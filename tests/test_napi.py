@@ -87,6 +87,16 @@ def test_addon_check_expert_weight(addon_report):
         assert re.search(rx, r["message"]) and r["message"].startswith("moeUp: "), (name, r)
 
 
+def test_addon_refuses_malformed_meta_and_wide_integers(addon_report):
+    got = dict(addon_report["malformed"])
+    want = {"rank 5": "at most 4 is supported", "fractional dim": "dims[0] must be a non-negative",
+            "string elems": "elems must be a non-negative integer",
+            "int64 overflow": "out of int64 range"}
+    for name, text in want.items():
+        r = got[name]
+        assert not r["ok"] and r["code"] == "INVALID_ARGUMENT" and text in r["message"], (name, r)
+
+
 def test_executor_dispatch_operands(tmp_path):
     src = open(os.path.join(NAPI, "hipExecutor.ts")).read()
     js = tmp_path / "hipExecutor.mjs"

@@ -57,6 +57,35 @@ def test_viterbi_transitions_follow_bioes():
     assert dec.start[I] == dec.NEG_INF and dec.end[B] == dec.NEG_INF
 
 
+def test_viterbi_rules_for_untagged_and_tagged_background_labels():
+    """Labels the v2 class list does not have, worked by hand from the rules
+    of viterbi.ts:39-77: a label with tag E but no span class (its moves are
+    those of a closed span, with the end biases), a label with a span class
+    but no tag (never entered), and a background token that carries span
+    class a with tag I (after B-a it continues the span, with the inside
+    bias)."""
+    info = pf.LabelInfo(
+        span_class_names=["O", "a"],
+        token_to_span_label={0: 0, 1: 1, 2: 1, 3: 1, 5: 1, 6: 1},
+        token_boundary_tags={1: "B", 2: "I", 3: "E", 4: "E", 6: "I"},
+        background_token_label=6, background_span_label=0, num_classes=7)
+    b = pf.ViterbiBiases(background_stay=1, background_to_start=2, inside_to_continue=3,
+                         inside_to_end=4, end_to_background=5, end_to_start=6)
+    t = pf.ViterbiDecoder(info, b).trans
+    NEG = pf.ViterbiDecoder.NEG_INF
+    # 4: tag E, no span class → may be followed by background or B/S
+    assert t[4, 0] == 5 and t[4, 6] == 5 and t[4, 1] == 6 and t[4, 2] == NEG and t[4, 3] == NEG
+    # 5: span class, no tag → never a next label; as a previous label it
+    # opens like background but with no bias
+    assert all(t[p, 5] == NEG for p in range(7))
+    assert t[5, 0] == 0 and t[5, 1] == 0 and t[5, 2] == NEG
+    # 6: the background token, span class a, tag I
+    assert t[1, 6] == 3 and t[2, 6] == 3       # continues the open span of class a
+    assert t[6, 6] == 1 and t[6, 0] == 1       # background to background
+    assert t[6, 1] == 2 and t[6, 2] == NEG     # background to a start only
+    assert t[3, 6] == 5 and t[3, 1] == 6       # after E-a
+
+
 def test_labels_to_spans():
     info = pf.build_label_info(pf.V2_NER_CLASS_NAMES)
     # O B I E O S, then a dangling I and an E without its B
