@@ -6,16 +6,17 @@
 //
 // act between the two products is private to the layer. The gate/up GEMM
 // writes every f32 act value v as the 24-bit fixed-point integer
-// V = rint(v · 2^17) (|act| ≤ 56 by the clamped SwiGLU, so |V| < 2^23; the
-// rounding error, 2^-18 absolute, is three orders below the f16 hi + lo
-// split's contribution to the 2e-3 output bar), stored as three signed
-// bytes with V = 65536·h + 256·m + l. Down then runs three exact
-// v_mfma_i32_32x32x32_i8 per product (limbs h, m, l against the int8
-// weights, i32 accumulation: |Σ| ≤ 128·127·K, below 2^31 for K < 132,000)
-// and adds the limbs in the epilogue in f32. Against the f16 hi + lo form
-// this is 3 int8 MFMAs (each half an f16 MFMA's time) instead of 4 f16 per
-// 32 k, and the weights feed the matrix cores as loaded: no int8 → f16
-// conversion at all.
+// V = rint(v · 2^17) (|act| ≤ 56 by the clamped SwiGLU, so |V| < 2^23),
+// stored as three signed bytes with V = 65536·h + 256·m + l. The rounding
+// error is at most 2^-18 per act value; through K = 5632 weights of
+// |q·scale| ~ 0.09 it moves an output by ~1.5e-5 (rms), far inside the
+// 2e-3 bar, where f16 act alone (11 bits) would move it by ~7e-3. Down runs
+// three exact v_mfma_i32_32x32x32_i8 per product (limbs h, m, l against the
+// int8 weights, i32 accumulation: |Σ| ≤ 128·127·K, below 2^31 for
+// K < 132,000) and adds the limbs exactly in the epilogue (int64), rounding
+// once to f32. Against the f16 hi + lo form this is 3 int8 MFMAs (each half
+// an f16 MFMA's time) instead of 4 f16 per 32 k, and the weights feed the
+// matrix cores as loaded: no int8 → f16 conversion at all.
 //
 // The limbs: W = V + 32896 as a 24-bit two's complement integer has bytes
 // b0, b1, b2; l = b0 ^ 0x80 and m = b1 ^ 0x80 read as signed bytes are
@@ -283,13 +284,13 @@ void k_gemm_down_i8(I8Args p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int row = 32 * rg + 8 * (r / 4) + 4 * hf + (r % 4);
+      // the exact sum 65536·h + 256·m + l (int64), rounded once to f32
       floatx4 o;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        float v = (float)acc[c][0][r] * 65536.0f;
-        v = __builtin_fmaf((float)acc[c][1][r], 256.0f, v);
-        v += (float)acc[c][2][r];
-        o[c] = __builtin_fmaf(v, sc[c], bs[c]);
+        const int64_t v = ((int64_t)acc[c][0][r] << 16) + ((int64_t)acc[c][1][r] << 8) +
+                          (int64_t)acc[c][2][r];
+        o[c] = __builtin_fmaf((float)v, sc[c], bs[c]);
       }
       const uint32_t off = (row < rows && col_ok)
                                ? ((uint32_t)rowmap[row] * (uint32_t)p.N + (uint32_t)col) * 4u
