@@ -1,8 +1,9 @@
-"""The fused prefill layer (f16 x, both products on the grouped GEMM, act
-between them as int8 limbs and down on the int8 matrix cores) against the CPU
-oracle on every token, at shapes that exercise its tiling: partial 64-row
-blocks, a last N-tile narrower than 512 columns, experts with no rows, a
-hot expert, K with an odd number of step pairs.
+"""The fused prefill layer (both products on the grouped GEMM; with f16 x act
+goes between them as int8 limbs and down runs on the int8 matrix cores)
+against the CPU oracle on every token, at shapes that exercise its tiling:
+partial 64-row blocks, a last N-tile narrower than 512 columns, experts with
+no rows, a hot expert, K with an odd number of step pairs, and the f16 hi +
+lo pairs form that f32 x and I not a multiple of 64 take.
 
 Bar: expert ids bit-exact, outputs within 2e-3 + 1e-2·|want| of the oracle
 (the north star's layer bar)."""
@@ -23,6 +24,11 @@ SHAPES = [
     MoeConfig("p_ragged", 300, 640, 6, 4, 384, "f16"),          # d = 640: N-tile of 128 columns
     MoeConfig("p_oddpairs", 384, 640, 5, 2, 448, "f16"),        # 7 step pairs
     MoeConfig("p_skew", 512, 640, 16, 2, 384, "f16", zipf=1.2, hot_share=0.5, empty=2),
+    # the layer's other prefill forms: f32 x (act as f16 hi + lo pairs, down
+    # on the f16 matrix cores), and f16 x with I not a multiple of 64 (the
+    # same pairs form: int8 limbs need whole step pairs)
+    MoeConfig("p_f32x", 512, 1024, 8, 2, 1024, "f32"),
+    MoeConfig("p_i1056", 512, 1024, 8, 2, 1056, "f16"),
 ]
 
 
