@@ -158,14 +158,18 @@ __device__ __forceinline__ uint32_t swap8(uint32_t v) {
 // sums wait in LDS for the SwiGLU epilogue.
 // GROUPED: scales change along K (groupSize < K), so partial sums are
 // scaled per group; otherwise one scale per column is applied at the end.
-// KS = 2 splits every stream over two wavefronts, each taking half of K
-// (more wavefronts in flight when few experts and columns are active); at
-// each segment end the second half's sums meet the first's in LDS, added as
-// first + second, before the scales, biases and SwiGLU.
+// KS = 2 or 4 splits every stream over KS wavefronts, each taking a
+// contiguous 1/KS of K (more wavefronts, and more of each stream's loads in
+// flight at once, when few experts and columns are active); at each segment
+// end the later parts' sums meet the first's in LDS, added in part order,
+// before the scales, biases and SwiGLU.
 // NWS streams per block; the block has NW = NWS·KS wavefronts.
 // Weight stream buffers per wavefront (loads SK_PD − 1 steps ahead). 6 and 8
 // measured slower at configs 2 and 3 (fewer wavefronts fit), up to 25%.
 constexpr int SK_PD = 4;
+#ifndef SKINNY_KS4_STREAMS
+#define SKINNY_KS4_STREAMS 256
+#endif
 // NORM: gate/up of moe_block with the pre-norm applied while staging
 // (a_inv, a_normw); a template flag, so that the instances without it keep
 // their registers.
@@ -173,7 +177,8 @@ template <int MODE, typename AT, bool GROUPED, int NWS, int NS, int KS, bool NOR
 __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(NS == 1 ? 3 : 4))) void k_expert_skinny(
     ExpertKArgs p) {
   constexpr int NW = NWS * KS;
-  static_assert(KS == 1 || (KS == 2 && !GROUPED), "K split only with one scale per column");
+  static_assert(KS == 1 || ((KS == 2 || KS == 4) && !GROUPED),
+                "K split only with one scale per column");
   // Up with NS = 2: one wavefront streams glu then lin of its column group.
   // Up with NS = 1: glu and lin on paired wavefronts (2w, 2w+1), which meet
   // in LDS after the stream. Down: NS column groups per wavefront.
@@ -198,7 +203,7 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = threadIdx.x / WAVE;
   const int sw = wave / KS;     // stream of this wavefront
-  const int kpart = wave % KS;  // its half of K when split
+  const int kpart = wave % KS;  // its part of K when split
   const int N4 = p.N / 4, K4 = p.K / 4;
   const int arr = PAIRED ? (sw & 1) : 0;  // weight array of a paired stream
   const int cg0 = PAIRED ? blockIdx.x * (NWS / 2) + (sw >> 1)
@@ -223,9 +228,10 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
   _Float16 *alo = ahi + RC * kp;
   floatx4 *park0 = (floatx4 *)(smem + (size_t)RC * kp * 2 * planes);
   floatx4 *park = park0 + (PAIRED ? (sw >> 1) : sw) * 4 * WAVE;
-  // K-split partial sums, one [4][64] floatx4 slot per stream, after the parks.
+  // K-split partial sums, KS − 1 [4][64] floatx4 slots per stream, after the
+  // parks.
   floatx4 *red = park0 + (MODE == MODE_UP ? (PAIRED ? NWS / 2 : NWS) : 0) * 4 * WAVE +
-                 sw * 4 * WAVE;
+                 sw * (KS - 1) * 4 * WAVE;
 
   // Loaded units: instruction 0 takes unit 16·cg + (lane & 7), instruction 1
   // unit 16·cg + 8 + (lane & 7); tile (lane >> 3) of the step, ^ 1 for
@@ -390,19 +396,22 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
 
     // tot[i][q]: row 4·kq + q of the chunk, column 4·useg + i.
     auto finish = [&](int seg) {
-      if (KS == 2) {
-        // The second half parks its sums; the first adds them (first + second).
-        if (kpart == 1) {
+      if (KS > 1) {
+        // The later parts park their sums; the first adds them in part
+        // order ((first + second) + third) + ….
+        if (kpart > 0) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) red[i * WAVE + lane] = tot[i];
+          for (int i = 0; i < 4; i++) red[((kpart - 1) * 4 + i) * WAVE + lane] = tot[i];
         }
         __syncthreads();
         if (kpart == 0) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) tot[i] = tot[i] + red[i * WAVE + lane];
+          for (int j = 0; j < KS - 1; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) tot[i] = tot[i] + red[(j * 4 + i) * WAVE + lane];
         }
         __syncthreads();
-        if (kpart == 1) {
+        if (kpart > 0) {
 #pragma unroll
           for (int i = 0; i < 4; i++) tot[i] = floatx4{0.f, 0.f, 0.f, 0.f};
           return;
@@ -716,11 +725,14 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     const long streams = (long)ea.calls * max_active *
                          ((ncg + cg_per_block - 1) / cg_per_block) * nw;
     const int steps = (ea.K + 31) / 32;
-    const int ks = (!grouped && steps % 2 == 0 && streams < 1024) ? 2 : 1;
+    int ks = (!grouped && steps % 2 == 0 && streams < 1024) ? 2 : 1;
+    // Very few streams (one single-token call): four wavefronts per stream,
+    // so that each one's loads are nearly all in flight at once.
+    if (ks == 2 && steps % 4 == 0 && streams < SKINNY_KS4_STREAMS && nw <= 2) ks = 4;
     dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw * ks);
     // Up parks one [4][64] floatx4 per stream (per pair when paired).
     const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
-    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, ks == 2 ? nw : 0);
+    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, nw * (ks - 1));
 #define SKINNY(AT_, GR_, NW_, NS_, KS_)                                                   \
   do {                                                                                    \
     if constexpr (MODE == MODE_UP) {                                                      \
@@ -733,7 +745,8 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
   } while (0)
 #define SKINNY_KS(AT_, GR_, NW_, NS_)                                                     \
   if constexpr (!GR_) {                                                                   \
-    if (ks == 2) { SKINNY(AT_, GR_, NW_, NS_, 2); } else { SKINNY(AT_, GR_, NW_, NS_, 1); } \
+    if (ks == 4) { if constexpr (NW_ <= 2) { SKINNY(AT_, GR_, NW_, NS_, 4); } }             \
+    else if (ks == 2) { SKINNY(AT_, GR_, NW_, NS_, 2); } else { SKINNY(AT_, GR_, NW_, NS_, 1); } \
   } else { SKINNY(AT_, GR_, NW_, NS_, 1); }
 #define SKINNY_NS(AT_, GR_, NW_)                                                          \
   if (ns == 2) { SKINNY_KS(AT_, GR_, NW_, 2); }                                           \
