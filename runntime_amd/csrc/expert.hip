@@ -54,6 +54,9 @@ struct ExpertKArgs {
   float *out;
   int64_t out_cs;
   int rc;  // rows staged per chunk (skinny kernel)
+  // act in dispatch order (fused layer): up writes row p of the sorted
+  // order, down reads it there, so neither waits on perm for those rows.
+  int sorted;
   DispatchBufs db;
   const float *a_inv;   // moe_block's pre-norm (up, skinny kernel), or NULL
   const void *a_normw;
@@ -296,7 +299,9 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
       constexpr int NT = 64 * NW;
       const int cpr = kp / EPC;  // pieces per staged row (kp is a multiple of 8)
       const int total = RC * cpr;
-      const int srcv = lane < rows ? perm[p0 + c0 + lane] / p.a_row_div : 0;
+      const int srcv = lane >= rows ? 0
+                       : (MODE == MODE_DOWN && p.sorted) ? p0 + c0 + lane
+                                                         : perm[p0 + c0 + lane] / p.a_row_div;
       const bool vec = p.K % EPC == 0 && (((uintptr_t)abase) & 15) == 0;
       const AT *nw = (const AT *)p.a_normw;
       const bool nvec = vec && (((uintptr_t)nw) & 15) == 0;
@@ -382,7 +387,7 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int mm = kq * 4 + q;
-      orow_i[q] = mm < rows ? perm[p0 + c0 + mm] : 0;
+      orow_i[q] = mm >= rows ? 0 : (MODE == MODE_UP && p.sorted) ? p0 + c0 + mm : perm[p0 + c0 + mm];
     }
     __syncthreads();
 
@@ -571,7 +576,10 @@ __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
   if (n >= p.N) return;
   const int64_t asg = p.db.perm[call * p.db.perm_cs() + pos];
   const int e = route_expert(p.route + call * p.route_cs, asg, p.k, p.E);
-  const AT *x = (const AT *)p.a + call * p.a_cs + (asg / p.a_row_div) * p.K;
+  // Sorted act: down reads, up writes, the row at the dispatch position.
+  const int64_t arow = (MODE == MODE_DOWN && p.sorted) ? pos : asg / p.a_row_div;
+  const int64_t orow = (MODE == MODE_UP && p.sorted) ? pos : asg;
+  const AT *x = (const AT *)p.a + call * p.a_cs + arow * p.K;
   const int kg = p.K / p.g;
   float acc[2] = {0.f, 0.f};
   constexpr int NARR = (MODE == MODE_UP) ? 2 : 1;
@@ -597,7 +605,7 @@ __global__ __launch_bounds__(256) void k_expert_simple(ExpertKArgs p) {
   } else {
     v = acc[0] + (b0 ? b0[(int64_t)e * p.N + n] : 0.f);
   }
-  p.out[call * p.out_cs + asg * p.N + n] = v;
+  p.out[call * p.out_cs + orow * p.N + n] = v;
 }
 
 // out[t] = residual[t] + Σ_s gate_s · y[t·k + s], slots in order; rows of
@@ -806,9 +814,8 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   if (db.E != ea.E || db.A != ea.A)
     return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch workspace sized for another shape");
   if (expert_uses_gemm(ea)) return launch_expert_gemm(ea, db, s);
-  if (ea.dispatch_order)
-    return moe_fail(MOE_EXECUTION_FAILED, "expert: dispatch-order rows need the grouped GEMM");
   ExpertKArgs p;
+  p.sorted = ea.dispatch_order;
   p.a = ea.a;
   p.a_cs = ea.a_cs;
   p.a_row_div = ea.a_row_div;

@@ -662,6 +662,9 @@ static int layer_impl(const char *op, moe_ctx *ctx, int calls, const moe_call_st
     }
   } else {
     dn.parts = 1;
+    // Both on the decode kernels: act in dispatch order too (f32), so down
+    // stages its rows without waiting on the permutation.
+    if (!expert_uses_gemm(up) && !expert_uses_gemm(dn)) up.dispatch_order = dn.dispatch_order = 1;
   }
   dn.out_cs = (int64_t)dn.parts * A * d;
 

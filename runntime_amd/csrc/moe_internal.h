@@ -183,10 +183,11 @@ struct ExpertArgs {
   int calls;
   // Intermediate rows in dispatch (sorted) order instead of assignment
   // order: up writes act row p for sorted position p, down reads it there.
-  // Only the grouped GEMM honours it (the fused layer sets it for both
-  // products when both run on the GEMM). Such act is private to the two
-  // products: each f32 value is stored as its f16 hi + lo split (the operands
-  // down's MFMAs take), hi(n), hi(n + 1), lo(n), lo(n + 1) per column pair.
+  // The fused layer sets it for both products when both run on the grouped
+  // GEMM or both on the decode kernels. Such act is private to the two
+  // products: on the grouped GEMM each f32 value is stored as its f16 hi +
+  // lo split (the operands down's MFMAs take), hi(n), hi(n + 1), lo(n),
+  // lo(n + 1) per column pair; on the decode kernels it stays f32.
   int dispatch_order;
   // Down on the grouped GEMM: K split into `parts` halves whose partial
   // products go to out + part·A·N (the combine adds them). 0 or 1 = whole K.
