@@ -128,7 +128,8 @@ def test_moe_block_matches_oracle(cid, sample):
 
 
 @pytest.mark.parametrize("cid,T,x_dtype", [(1, None, None), (3, None, None), (2, 100, None),
-                                           (2, 100, "f16"), (2, 40, "f16"), (4, None, None)])
+                                           (2, 100, "f16"), (2, 40, "f16"), (2, None, "f16"),
+                                           (4, None, None)])
 def test_moe_block_is_norm_then_layer(cid, T, x_dtype):
     """moe_block = rmsNorm → moe_layer(xn) with residual x, bit for bit.
     The block normalises x while staging it for calls of at most 64 tokens

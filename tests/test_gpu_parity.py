@@ -375,6 +375,29 @@ def test_moe_layer_configs(cid, sample):
     assert all(len(set(r)) == k for r in ids.tolist())
 
 
+@pytest.mark.parametrize("T,d,E,k,I,x_dtype", [(1, 640, 128, 4, 640, "f16"), (1, 640, 128, 4, 640, "f32"),
+                                               (2, 512, 8, 2, 1024, "f32"), (1, 2048, 64, 8, 1408, "f16"),
+                                               (3, 256, 16, 4, 384, "f16")])
+def test_moe_layer_small_calls(T, d, E, k, I, x_dtype):
+    """Single-token and few-token calls, where the decode kernels split each
+    weight stream over four (or two) wavefronts and keep act in dispatch
+    order between the products: every token against the oracle."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS[2], name="small", T=T, d=d, E=E, k=k, I=I, x_dtype=x_dtype)
+    say(f"moe_layer small call T={T} d={d} E={E} k={k} I={I} {x_dtype}")
+    inp = make_inputs(cfg, seed=40 + T, keep_q=True, bias_rand=True)
+    g = torch.Generator().manual_seed(41)
+    inp.residual.copy_(torch.randn(tuple(inp.residual.shape), generator=g))
+    out, route = rt.moe_layer(inp.x, inp.router_w, inp.router_b, inp.glu, inp.lin, inp.down,
+                              inp.residual, k, return_route=True)
+    got_out, got_route = host(out), host(route)
+    tokens = np.arange(T)
+    want_route, want_out, _ = _oracle_layer(inp, tokens)
+    assert np.array_equal(got_route[:, :k], want_route[:, :k]), "expert ids differ"
+    np.testing.assert_allclose(got_route[:, k:], want_route[:, k:], atol=1e-7, rtol=1e-5)
+    assert_close(got_out, want_out, what="small call output")
+
+
 @pytest.mark.parametrize("T,E,k,x_dtype", [(64, 64, 16, "f32"), (17, 32, 8, "f16"),
                                            (64, 128, 4, "f32"), (65, 16, 4, "f32")])
 def test_moe_layer_fused_router_dispatch_limits(T, E, k, x_dtype):
