@@ -12,8 +12,8 @@
 // |q·scale| ~ 0.09 it moves an output by ~1.5e-5 (rms), far inside the
 // 2e-3 bar, where f16 act alone (11 bits) would move it by ~7e-3. Down runs
 // three exact v_mfma_i32_32x32x32_i8 per product (limbs h, m, l against the
-// int8 weights, i32 accumulation: |Σ| ≤ 128·127·K, below 2^31 for
-// K < 132,000) and adds the limbs exactly in the epilogue (int64), rounding
+// int8 weights, i32 accumulation: |Σ| ≤ 128·128·K, below 2^31 for
+// K < 131,072) and adds the limbs exactly in the epilogue (int64), rounding
 // once to f32. Against the f16 hi + lo form this is 3 int8 MFMAs (each half
 // an f16 MFMA's time) instead of 4 f16 per 32 k, and the weights feed the
 // matrix cores as loaded: no int8 → f16 conversion at all.
@@ -306,10 +306,12 @@ void k_gemm_down_i8(I8Args p) {
 
 bool gemm_i8_down_eligible(const ExpertArgs &dn) {
   // 8-bit weights with one scale group per column, K in whole step pairs
-  // with at least a ring's worth of them, 32-bit buffer offsets.
+  // with at least a ring's worth of them, 32-bit buffer offsets, and i32
+  // limb sums that cannot overflow (|limb · q| ≤ 128 · 128 per k).
   const int64_t mt = (dn.A + BM - 1) / BM + (dn.E < dn.A ? dn.E : dn.A);
   return dn.mode == MODE_DOWN && dn.bits == 8 && dn.g == dn.K && dn.K % 64 == 0 &&
-         dn.K / 64 >= I8_SPA && dn.N % 4 == 0 && dn.E <= I8_MAX_E && dn.calls == 1 &&
+         dn.K / 64 >= I8_SPA && dn.K < (1 << 17) && dn.N % 4 == 0 && dn.E <= I8_MAX_E &&
+         dn.calls == 1 &&
          gemm_i8_act_bytes(dn.A, dn.E, dn.K) < (1ll << 31) &&
          (int64_t)dn.A * dn.N * 4 < (1ll << 31) && (int64_t)dn.K * dn.N < (1ll << 31) &&
          mt > 0;
