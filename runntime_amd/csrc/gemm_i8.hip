@@ -71,6 +71,10 @@ constexpr int I8_PAIR = I8_BM * 64 * 3;          // act bytes of one pair: 12 KB
 constexpr int I8_LOADS = 6;                      // loads per wavefront and pair (2 act, 4 weights)
 constexpr int I8_WPAIR = 4 * 2 * 32 * 128;        // weights of one pair: 32 KB
 constexpr int I8_MAX_E = GEMM_MAX_E;
+// Offset past every buffer: a load there fetches nothing (the range check
+// drops it) and lands zeros in the junk area; keeps each wavefront's load
+// count fixed without moving bytes.
+constexpr uint32_t I8_NOFETCH = 0x80000000u;
 
 struct I8Args {
   const uint8_t *act;      // limbs, layout above
@@ -164,16 +168,17 @@ void k_gemm_down_i8(I8Args p) {
     if (tid < I8_BM) rowmap[tid] = p.perm[r0 + min(tid, rows - 1)];
 
     // Loads of a pair, 6 per wavefront: act chunks 2w, 2w + 1 (12 chunks of
-    // 1 KB over wavefronts 0-5; wavefronts 6 and 7 load into the junk area
-    // so that every wavefront issues the same count), then the weights of
-    // step rg of the pair for units 32·cg .. 32·cg + 31: instruction i loads
-    // units 8i .. 8i + 7 of the group, lane l the 16-byte chunk
-    // (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes, so that chunk c
-    // of unit u sits at u·128 + (c ^ sw8(u))·16 (the 16 lanes reading one
-    // tile of 16 units hit 16 different bank groups). A unit past N reads
-    // the last unit (its outputs are not stored). Past the last pair every
-    // load goes to the junk area. Branch-free: a load under a branch makes
-    // the compiler wait for every load in flight where the paths join.
+    // 1 KB over wavefronts 0-5; wavefronts 6 and 7 issue fetch-free loads
+    // into the junk area, so that every wavefront issues the same count),
+    // then the weights of step rg of the pair for units 32·cg .. 32·cg + 31:
+    // instruction i loads units 8i .. 8i + 7 of the group, lane l the
+    // 16-byte chunk (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes,
+    // so that chunk c of unit u sits at u·128 + (c ^ sw8(u))·16 (the 16
+    // lanes reading one tile of 16 units hit 16 different bank groups). A
+    // unit past N loads from past the buffer (zeros, no fetch; its outputs
+    // are not stored). Past the last pair every load goes to the junk area
+    // from there too. Branch-free: a load under a branch makes the
+    // compiler wait for every load in flight where the paths join.
     const uint32_t a_base = (uint32_t)blk * (uint32_t)npairs * (uint32_t)I8_PAIR;
     const i32x4 wr = buffer_rsrc(p.w + (uint64_t)e * slab, (uint32_t)slab);
     uint32_t woff[4];
@@ -182,8 +187,9 @@ void k_gemm_down_i8(I8Args p) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int uu = 8 * i + (ln >> 3);
-        const int ug = min(U0 + 32 * cg + uu, N4 - 1);
-        woff[i] = (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u;
+        const int ug = U0 + 32 * cg + uu;
+        woff[i] = ug < N4 ? (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u
+                          : I8_NOFETCH;
       }
     }
     auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
@@ -192,11 +198,11 @@ void k_gemm_down_i8(I8Args p) {
         const bool ok = ja < npairs && c < 12;
         const uint32_t at = a_base + (uint32_t)ja * I8_PAIR + (uint32_t)c * 1024u +
                             (uint32_t)fresh_lane_i8() * 16u;
-        dma16(ar, ok ? at : 0u, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
+        dma16(ar, ok ? at : I8_NOFETCH, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
       } else {
         const int i = n - 2;
         const bool ok = jw >= 0 && jw < npairs;
-        dma16(wr, woff[i], ok ? (2 * jw + rg) * (BK * 4) : 0,
+        dma16(wr, ok ? woff[i] : I8_NOFETCH, ok ? (2 * jw + rg) * (BK * 4) : 0,
               ok ? wring0 + sw_ * I8_WPAIR + cg * 8192 + rg * 4096 + i * 1024 : junk0);
       }
     };
