@@ -102,7 +102,7 @@ void k_gemm_down_i8(I8Args p) {
   __shared__ __align__(16) uint8_t aring[I8_SPA * I8_PAIR];   // 48 KB
   __shared__ __align__(16) uint8_t wring[I8_SPW * I8_WPAIR];  // 96 KB
   __shared__ __align__(16) uint8_t junk[1024];
-  __shared__ int32_t rowmap[I8_BM];
+  __shared__ int32_t rowmap[2][I8_BM];  // this tile's and the next one's
   __shared__ int4 descs[I8_MAX_E];
   __shared__ int c64[I8_MAX_E + 1];  // cumulative 64-row blocks per active expert
 
@@ -147,9 +147,17 @@ void k_gemm_down_i8(I8Args p) {
   const __amdgpu_buffer_rsrc_t yrc = __builtin_amdgcn_make_buffer_rsrc(p.y, 0, p.y_bytes, BUF_DWORD3);
   const int swu = sw8(u);
 
-  for (int L = start; L < end; L += bx) {
-    // ---- the tile: expert (binary search over the block counts), N-tile,
-    // row block. Tiles of active expert i: c64[i]·nt .. c64[i + 1]·nt.
+  // ---- a tile: expert (binary search over the block counts), N-tile, row
+  // block. Tiles of active expert i: c64[i]·nt .. c64[i + 1]·nt. Past the
+  // block's range a tile is invalid and only its loads' validity is read.
+  struct TileP {
+    int e, r0, rows, U0;
+    uint32_t a_base;  // act bytes of the tile's row block
+    bool valid;
+  };
+  auto decode = [&](int L) {
+    TileP T{0, 0, 1, 0, 0u, false};
+    if (L >= end) return T;
     int lo = 0, hi = n_active - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -159,91 +167,123 @@ void k_gemm_down_i8(I8Args p) {
     const int nb = c64[lo + 1] - c64[lo];
     const int local = L - c64[lo] * p.nt;
     const int ntile = local / nb, jb = local % nb;
-    const int e = __builtin_amdgcn_readfirstlane(d.x);
-    const int r0 = __builtin_amdgcn_readfirstlane(d.y + jb * I8_BM);  // first sorted row
-    const int rows = __builtin_amdgcn_readfirstlane(min(I8_BM, d.z - jb * I8_BM));
-    const int blk = __builtin_amdgcn_readfirstlane(2 * d.w + jb);    // act block
-    const int U0 = ntile * I8_UNITS;
+    T.e = __builtin_amdgcn_readfirstlane(d.x);
+    T.r0 = __builtin_amdgcn_readfirstlane(d.y + jb * I8_BM);  // first sorted row
+    T.rows = __builtin_amdgcn_readfirstlane(min(I8_BM, d.z - jb * I8_BM));
+    T.U0 = ntile * I8_UNITS;
+    const int blk = __builtin_amdgcn_readfirstlane(2 * d.w + jb);  // act block
+    T.a_base = (uint32_t)blk * (uint32_t)npairs * (uint32_t)I8_PAIR;
+    T.valid = true;
+    return T;
+  };
 
-    if (tid < I8_BM) rowmap[tid] = p.perm[r0 + min(tid, rows - 1)];
-
-    // Loads of a pair, 6 per wavefront: act chunks 2w, 2w + 1 (12 chunks of
-    // 1 KB over wavefronts 0-5; wavefronts 6 and 7 issue fetch-free loads
-    // into the junk area, so that every wavefront issues the same count),
-    // then the weights of step rg of the pair for units 32·cg .. 32·cg + 31:
-    // instruction i loads units 8i .. 8i + 7 of the group, lane l the
-    // 16-byte chunk (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes,
-    // so that chunk c of unit u sits at u·128 + (c ^ sw8(u))·16 (the 16
-    // lanes reading one tile of 16 units hit 16 different bank groups). A
-    // unit past N loads from past the buffer (zeros, no fetch; its outputs
-    // are not stored). Past the last pair every load goes to the junk area
-    // from there too. Branch-free: a load under a branch makes the
-    // compiler wait for every load in flight where the paths join.
-    const uint32_t a_base = (uint32_t)blk * (uint32_t)npairs * (uint32_t)I8_PAIR;
-    const i32x4 wr = buffer_rsrc(p.w + (uint64_t)e * slab, (uint32_t)slab);
-    uint32_t woff[4];
-    {
-      const int ln = fresh_lane_i8();
+  // Loads of a pair, 6 per wavefront: act chunks 2w, 2w + 1 (12 chunks of
+  // 1 KB over wavefronts 0-5; wavefronts 6 and 7 issue fetch-free loads into
+  // the junk area, so that every wavefront issues the same count), then the
+  // weights of step rg of the pair for units 32·cg .. 32·cg + 31:
+  // instruction i loads units 8i .. 8i + 7 of the group, lane l the 16-byte
+  // chunk (l & 7) ^ sw8(unit) of unit 8i + (l >> 3)'s 128 bytes, so that
+  // chunk c of unit u sits at u·128 + (c ^ sw8(u))·16 (the 16 lanes reading
+  // one tile of 16 units hit 16 different bank groups). A unit past N loads
+  // from past the buffer (zeros, no fetch; its outputs are not stored).
+  // Pairs past a tile's last are the next tile's first (the ring runs on
+  // across the block's tiles); past the block's last tile every load goes
+  // to the junk area, fetch-free. Branch-free: a load under a branch makes
+  // the compiler wait for every load in flight where the paths join.
+  auto woffs = [&](const TileP &T, uint32_t (&wo)[4]) {
+    const int ln = fresh_lane_i8();
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int uu = 8 * i + (ln >> 3);
-        const int ug = U0 + 32 * cg + uu;
-        woff[i] = ug < N4 ? (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u
-                          : I8_NOFETCH;
-      }
+    for (int i = 0; i < 4; i++) {
+      const int uu = 8 * i + (ln >> 3);
+      const int ug = T.U0 + 32 * cg + uu;
+      wo[i] = ug < N4 ? (uint32_t)ug * (uint32_t)p.K * 4u + (uint32_t)((ln & 7) ^ sw8(uu)) * 16u
+                      : I8_NOFETCH;
     }
-    auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
-      if (n < 2) {
-        const int c = 2 * wave + n;
-        const bool ok = ja < npairs && c < 12;
-        const uint32_t at = a_base + (uint32_t)ja * I8_PAIR + (uint32_t)c * 1024u +
-                            (uint32_t)fresh_lane_i8() * 16u;
-        dma16(ar, ok ? at : I8_NOFETCH, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
-      } else {
-        const int i = n - 2;
-        const bool ok = jw >= 0 && jw < npairs;
-        dma16(wr, ok ? woff[i] : I8_NOFETCH, ok ? (2 * jw + rg) * (BK * 4) : 0,
-              ok ? wring0 + sw_ * I8_WPAIR + cg * 8192 + rg * 4096 + i * 1024 : junk0);
-      }
-    };
-    auto issue_pair = [&](int ja, int sa_, int jw, int sw_) {
+  };
+  TileP T = decode(start), Tn = decode(start + bx);  // this tile, the next
+  uint32_t woff[4], woffn[4];
+  woffs(T, woff);
+  woffs(Tn, woffn);
+  i32x4 wr = buffer_rsrc(p.w + (uint64_t)T.e * slab, (uint32_t)slab);
+  i32x4 wrn = buffer_rsrc(p.w + (uint64_t)Tn.e * slab, (uint32_t)slab);
+
+  // Pair ja of act, jw of the weights, counted from this tile's first
+  // (≥ npairs: the next tile's).
+  auto issue_one = [&](int n, int ja, int sa_, int jw, int sw_) {
+    if (n < 2) {
+      const int c = 2 * wave + n;
+      const bool nx = ja >= npairs;
+      const int jj = nx ? ja - npairs : ja;
+      const bool ok = (nx ? Tn.valid : T.valid) && c < 12;
+      const uint32_t at = (nx ? Tn.a_base : T.a_base) + (uint32_t)jj * I8_PAIR +
+                          (uint32_t)c * 1024u + (uint32_t)fresh_lane_i8() * 16u;
+      dma16(ar, ok ? at : I8_NOFETCH, 0, ok ? aring0 + sa_ * I8_PAIR + c * 1024 : junk0);
+    } else {
+      const int i = n - 2;
+      const bool nx = jw >= npairs;
+      const int jj = nx ? jw - npairs : jw;
+      const bool ok = (nx ? Tn.valid : T.valid) && jj >= 0;
+      dma16(nx ? wrn : wr, ok ? (nx ? woffn[i] : woff[i]) : I8_NOFETCH,
+            ok ? (2 * jj + rg) * (BK * 4) : 0,
+            ok ? wring0 + sw_ * I8_WPAIR + cg * 8192 + rg * 4096 + i * 1024 : junk0);
+    }
+  };
+  auto issue_pair = [&](int ja, int sa_, int jw, int sw_) {
 #pragma unroll
-      for (int n = 0; n < I8_LOADS; n++) issue_one(n, ja, sa_, jw, sw_);
-    };
+    for (int n = 0; n < I8_LOADS; n++) issue_one(n, ja, sa_, jw, sw_);
+  };
+
+  // The pipeline: after the barrier of pair j (its loads landed, every read
+  // of pair j − 1 done), the act loads of pair j + SPA − 1 and the weight
+  // loads of pair j + SPW − 1 go into pair j − 1's stages, spread between
+  // the MFMA groups of step 2j (all wavefronts issuing them in one burst
+  // stalls the matrix cores together). At the wait of pair j, its weights
+  // (issued one pair after its act) are followed by exactly one pair's
+  // I8_LOADS younger instructions. The stages rotate over the block's whole
+  // run of pairs; only its first tile has a prologue, which issues virtual
+  // pairs −(SPA − 1) .. −1 of the same pattern.
+  static_assert(I8_SPA == I8_SPW + 1, "act runs one pair ahead of the weights");
+  if (T.valid) {
+#pragma unroll
+    for (int v = 0; v < I8_SPA - 1; v++) issue_pair(v, v, v - 1, v - 1);
+  }
+
+  // Fragments of step q of the pair: act rows 32·rg + u, limb l3, half hf;
+  // the unit's four quantW tiles for half hf (tile t = columns 0..3 × k
+  // 4t .. 4t + 3).
+  struct Frags {
+    u32x4 a[3];
+    u32x4 w[4];
+  };
+  auto read_frags = [&](Frags &F, int sa, int sw, int q) {
+    const uint8_t *s = aring + sa * I8_PAIR + hf * 1024 + (32 * rg + u) * 16 + q * 2048;
+#pragma unroll
+    for (int l3 = 0; l3 < 3; l3++) F.a[l3] = *(const u32x4 *)(s + l3 * 4096);
+    const uint8_t *t = wring + sw * I8_WPAIR + cg * 8192 + q * 4096 + u * 128;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; j4++) F.w[j4] = *(const u32x4 *)(t + ((hf * 4 + j4) ^ swu) * 16);
+  };
+
+  int sa = 0, sw = 0, rb = 0;
+  for (int L = start; L < end; L += bx) {
+    // ---- tile start: its row map and epilogue constants. Their one wait
+    // (the compiler's, for every load in flight) also covers this tile's
+    // first pairs, issued under the previous tile, and that tile's stores.
+    const int uo = T.U0 + 32 * cg + u;
+    const bool col_ok = uo < N4;
+    const int col = 4 * min(uo, N4 - 1);
+    const int rmv = tid < I8_BM ? p.perm[T.r0 + min(tid, T.rows - 1)] : 0;
+    const floatx4 sc = *(const floatx4 *)(p.scales + (size_t)T.e * p.N + col) * (1.0f / 131072.0f);
+    floatx4 bs = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) bs = *(const floatx4 *)(p.bias + (size_t)T.e * p.N + col);
+    if (tid < I8_BM) rowmap[rb][tid] = rmv;
+    asm volatile("" ::"v"(sc), "v"(bs));
 
     i32x16 acc[4][3];
 #pragma unroll
     for (int c = 0; c < 4; c++)
 #pragma unroll
       for (int l3 = 0; l3 < 3; l3++) acc[c][l3] = i32x16{};
-
-    // The pipeline: after the barrier of pair j (its loads landed, every
-    // read of pair j − 1 done), the act loads of pair j + SPA − 1 and the
-    // weight loads of pair j + SPW − 1 go into pair j − 1's stages, spread
-    // between the MFMA groups of step 2j (all wavefronts issuing them in one
-    // burst stalls the matrix cores together). At the wait of pair j, its
-    // weights (issued one pair after its act) are followed by exactly one
-    // pair's I8_LOADS younger instructions. The prologue issues virtual
-    // pairs −(SPA − 1) .. −1 of the same pattern.
-    static_assert(I8_SPA == I8_SPW + 1, "act runs one pair ahead of the weights");
-#pragma unroll
-    for (int v = 0; v < I8_SPA - 1; v++) issue_pair(v, v, v - 1, v - 1);
-
-    // Fragments of step q of the pair: act rows 32·rg + u, limb l3, half hf;
-    // the unit's four quantW tiles for half hf (tile t = columns 0..3 × k
-    // 4t .. 4t + 3).
-    struct Frags {
-      u32x4 a[3];
-      u32x4 w[4];
-    };
-    auto read_frags = [&](Frags &F, int sa, int sw, int q) {
-      const uint8_t *s = aring + sa * I8_PAIR + hf * 1024 + (32 * rg + u) * 16 + q * 2048;
-#pragma unroll
-      for (int l3 = 0; l3 < 3; l3++) F.a[l3] = *(const u32x4 *)(s + l3 * 4096);
-      const uint8_t *t = wring + sw * I8_WPAIR + cg * 8192 + q * 4096 + u * 128;
-#pragma unroll
-      for (int j4 = 0; j4 < 4; j4++) F.w[j4] = *(const u32x4 *)(t + ((hf * 4 + j4) ^ swu) * 16);
-    };
     // The 12 MFMAs of a step; hook(c) runs after column tile c's three.
     auto mfmas = [&](const Frags &F, auto hook) {
 #pragma unroll
@@ -258,7 +298,6 @@ void k_gemm_down_i8(I8Args p) {
       }
     };
 
-    int sa = 0, sw = 0;
     for (int j = 0; j < npairs; j++) {
       WAIT_VMCNT(I8_LOADS);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -276,17 +315,10 @@ void k_gemm_down_i8(I8Args p) {
       sa = sa + 1 == I8_SPA ? 0 : sa + 1;
       sw = sw + 1 == I8_SPW ? 0 : sw + 1;
     }
-    WAIT_VMCNT(0);
-    block_barrier();
 
     // ---- epilogue: y[assignment][col .. col + 3] = scale · V-sum · 2^-17
-    // + bias, for columns 4·unit' + 0..3 of the lane.
-    const int uo = U0 + 32 * cg + u;
-    const bool col_ok = uo < N4;
-    const int col = 4 * min(uo, N4 - 1);
-    const floatx4 sc = *(const floatx4 *)(p.scales + (size_t)e * p.N + col) * (1.0f / 131072.0f);
-    floatx4 bs = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias) bs = *(const floatx4 *)(p.bias + (size_t)e * p.N + col);
+    // + bias, for columns 4·unit' + 0..3 of the lane. The row map was
+    // written before this tile's first barrier.
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int row = 32 * rg + 8 * (r / 4) + 4 * hf + (r % 4);
@@ -298,14 +330,24 @@ void k_gemm_down_i8(I8Args p) {
                           (int64_t)acc[c][2][r];
         o[c] = __builtin_fmaf((float)v, sc[c], bs[c]);
       }
-      const uint32_t off = (row < rows && col_ok)
-                               ? ((uint32_t)rowmap[row] * (uint32_t)p.N + (uint32_t)col) * 4u
+      const uint32_t off = (row < T.rows && col_ok)
+                               ? ((uint32_t)rowmap[rb][row] * (uint32_t)p.N + (uint32_t)col) * 4u
                                : 0x80000000u;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), yrc, off, 0, 0);
     }
-    // rowmap and the stages are rewritten by the next tile.
-    block_barrier();
+    // ---- the next tile (its first pairs are in flight); the one after.
+    T = Tn;
+#pragma unroll
+    for (int i = 0; i < 4; i++) woff[i] = woffn[i];
+    wr = wrn;
+    Tn = decode(L + 2 * bx);
+    woffs(Tn, woffn);
+    wrn = buffer_rsrc(p.w + (uint64_t)Tn.e * slab, (uint32_t)slab);
+    rb ^= 1;
   }
+  // Loads past the last tile (fetch-free) still land in the junk area: wait
+  // for them before the workgroup's LDS goes away.
+  WAIT_VMCNT(0);
 }
 
 }  // namespace
