@@ -23,6 +23,7 @@
 namespace {
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4_r __attribute__((ext_vector_type(4)));
 constexpr int WAVE = 64;
 using moe_dev::wave_topk_route;
 
@@ -79,7 +80,10 @@ __device__ __forceinline__ void tile_rows_inv(const T *x, int64_t stride, int co
 
 // NORM: moe_block's pre-norm applied while staging (ra.norm_w); a template
 // flag, so that the plain instance keeps its few registers (occupancy).
-template <typename T, bool NORM>
+// VEC (E a multiple of 4): W comes in 16-byte loads, four experts a lane.
+// One CU's load instructions, not bytes, bound this kernel: 4-byte loads
+// move ~23 GB/s per CU (256 B per wavefront instruction).
+template <typename T, bool NORM, bool VEC>
 __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   __shared__ float xs[RT_TOKENS * ROUTER_CHUNK];
   __shared__ float ws[ROUTER_CHUNK * RT_EXPERTS];
@@ -99,7 +103,8 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   // Staging: every load of the tile is issued before the first LDS store.
   constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
   const T *nw = NORM ? (const T *)ra.norm_w : nullptr;
-  float xv[XPER], wv[WPER], nv[NORM ? XPER : 1];
+  float xv[XPER], nv[NORM ? XPER : 1];
+  floatx4_r wv[WPER / 4];
 #pragma unroll
   for (int r = 0; r < XPER; r++) {
     int i = threadIdx.x + 256 * r;
@@ -108,12 +113,27 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
     xv[r] = (t < Tn && kk < len) ? load_as_f32(x, (int64_t)t * d + k0 + kk) : 0.f;
     if constexpr (NORM) nv[r] = kk < len ? load_as_f32(nw, k0 + kk) : 0.f;
   }
+  if constexpr (VEC) {
+    // Lane i: experts 4(i mod 32) .. + 3 of k row i / 32 (et is a multiple of 4).
 #pragma unroll
-  for (int r = 0; r < WPER; r++) {
-    int i = threadIdx.x + 256 * r;
-    int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
-    wv[r] = (kk < len && ee < et) ? __builtin_nontemporal_load(w + (int64_t)(k0 + kk) * E + e0 + ee)
-                                  : 0.f;
+    for (int r = 0; r < WPER / 4; r++) {
+      int i = threadIdx.x + 256 * r;
+      int kk = i / (RT_EXPERTS / 4), ee = 4 * (i % (RT_EXPERTS / 4));
+      wv[r] = (kk < len && ee < et)
+                  ? __builtin_nontemporal_load((const floatx4_r *)(w + (int64_t)(k0 + kk) * E + e0 + ee))
+                  : floatx4_r{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < WPER / 4; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        int i = threadIdx.x + 256 * (4 * r + c);
+        int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
+        wv[r][c] = (kk < len && ee < et)
+                       ? __builtin_nontemporal_load(w + (int64_t)(k0 + kk) * E + e0 + ee)
+                       : 0.f;
+      }
   }
   // moe_block's pre-norm, while the tile's loads are in flight: wavefront w
   // takes the inverse RMS of the tile's tokens w, w + 4, w + 8, w + 12 (the
@@ -150,8 +170,15 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   }
 #pragma unroll
   for (int r = 0; r < XPER; r++) xs[threadIdx.x + 256 * r] = xv[r];
+  if constexpr (VEC) {
 #pragma unroll
-  for (int r = 0; r < WPER; r++) ws[threadIdx.x + 256 * r] = wv[r];
+    for (int r = 0; r < WPER / 4; r++) ((floatx4_r *)ws)[threadIdx.x + 256 * r] = wv[r];
+  } else {
+#pragma unroll
+    for (int r = 0; r < WPER / 4; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) ws[threadIdx.x + 256 * (4 * r + c)] = wv[r][c];
+  }
   __syncthreads();
   for (int p = threadIdx.x; p < RT_TOKENS * RT_EXPERTS; p += blockDim.x) {
     int tt = p / RT_EXPERTS, ee = p % RT_EXPERTS;
@@ -460,13 +487,19 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
     const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
     dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
+    // 16-byte W loads need every row of W 16-byte aligned.
+    const bool vec = ra.E % 4 == 0 && ((uintptr_t)ra.w & 15) == 0 && ra.w_cs % 4 == 0;
+#define RC_LAUNCH(T_, N_)                                                                      \
+  do {                                                                                         \
+    if (vec) hipLaunchKernelGGL((k_router_chunks<T_, N_, true>), grid, block, 0, s, ra);       \
+    else hipLaunchKernelGGL((k_router_chunks<T_, N_, false>), grid, block, 0, s, ra);          \
+  } while (0)
     if (ra.x_dtype == MOE_F16) {
-      if (ra.norm_w) hipLaunchKernelGGL((k_router_chunks<_Float16, true>), grid, block, 0, s, ra);
-      else hipLaunchKernelGGL((k_router_chunks<_Float16, false>), grid, block, 0, s, ra);
+      if (ra.norm_w) RC_LAUNCH(_Float16, true); else RC_LAUNCH(_Float16, false);
     } else {
-      if (ra.norm_w) hipLaunchKernelGGL((k_router_chunks<float, true>), grid, block, 0, s, ra);
-      else hipLaunchKernelGGL((k_router_chunks<float, false>), grid, block, 0, s, ra);
+      if (ra.norm_w) RC_LAUNCH(float, true); else RC_LAUNCH(float, false);
     }
+#undef RC_LAUNCH
   }
   const int ni = (ra.E + WAVE - 1) / WAVE;
   // Fold batch: the chunk count J, rounded up to 8, 16 or 32 (8 with more
