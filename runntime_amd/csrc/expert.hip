@@ -641,6 +641,12 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
 // time); the same order of operations per column.
 // Four residual values as f32.
 __device__ __forceinline__ float4 load4(const float *p) { return *(const float4 *)p; }
+// y is read once: nontemporal 16-byte loads (config 5's combine 60 → 52 µs).
+typedef float floatx4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load4_nt(const float *p) {
+  const floatx4_nt v = __builtin_nontemporal_load((const floatx4_nt *)p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ float4 load4(const _Float16 *p) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   const h4 v = *(const h4 *)p;
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y, i
     const int64_t asg = (int64_t)t * KK + s;
     ok[s] = route_expert(route, asg, KK, E) >= 0;
     gate[s] = route[(int64_t)t * 2 * KK + KK + s];
-    v[s] = *(const float4 *)&y[asg * N + n];
+    v[s] = load4_nt(&y[asg * N + n]);
   }
   // The residual after the slot loads, so they all wait together.
   float4 acc = residual ? load4(&residual[call * res_cs + (int64_t)t * N + n])
