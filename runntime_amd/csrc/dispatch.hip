@@ -35,12 +35,33 @@ __global__ __launch_bounds__(DBLOCK) void k_dispatch_count(const float *__restri
   for (int e = threadIdx.x; e < E; e += DBLOCK) cnt[e] = hist[e];
 }
 
+// Block counts staged in LDS when they fit: every load is then out at once
+// (summing them straight from memory waits one latency per few blocks).
+constexpr int SCAN_LDS_COUNTS = 8192;
+
 __global__ __launch_bounds__(1024) void k_dispatch_scan(DispatchBufs db, int tile_m) {
   __shared__ int32_t tot[DISPATCH_MAX_E];
   __shared__ int32_t off[DISPATCH_MAX_E + 1];
+  __shared__ int32_t cl[SCAN_LDS_COUNTS];
   const int call = blockIdx.x;
   const int E = db.E, nblk = db.nblk;
   const int32_t *cnt = db.blk_counts + call * db.cnt_cs();
+  const bool staged = nblk * E <= SCAN_LDS_COUNTS;
+  if (staged) {
+    // Up to eight counts a thread, all loaded before the first store (an
+    // index past the end reloads the last count, which is not stored).
+    const int n = nblk * E;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
+      int32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = cnt[min(i0 + u * (int)blockDim.x, n - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (i0 + u * (int)blockDim.x < n) cl[i0 + u * blockDim.x] = v[u];
+    }
+    __syncthreads();
+    cnt = cl;
+  }
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int32_t c = 0;
     for (int b = 0; b < nblk; b++) c += cnt[(int64_t)b * E + e];
