@@ -27,6 +27,7 @@
 
 #include "moe_internal.h"
 #include "norm_dev.h"
+#include "router_dev.h"
 
 namespace {
 
@@ -60,7 +61,105 @@ struct ExpertKArgs {
   DispatchBufs db;
   const float *a_inv;   // moe_block's pre-norm (up, skinny kernel), or NULL
   const void *a_normw;
+  // Up of single-token calls: the router's fold, top-k and dispatch in the
+  // prologue (fused_route), from the chunk sums; NULL otherwise.
+  const float *fr_partial;
+  const float *fr_b;
+  int64_t fr_b_cs;
+  int fr_J, fr_tile_m;
 };
+
+// Dynamic LDS fused_route borrows before the staging (int32 words).
+__host__ __device__ constexpr int fused_route_words(int E) { return 96 + 2 * E + 1; }
+
+// Single-token calls (p.fr_partial): the router's fold (chunk order, then
+// + b), top-k and the call's dispatch, recomputed by every block of the
+// call from its J·E chunk sums, so that no separate kernel sits between the
+// router's chunk kernel and this product. The fold and top-k are the
+// router's own (router_dev.h, bit for bit); block (0, 0) writes the route
+// row, perm and the dispatch buffers (offsets, M-tiles, active experts,
+// meta) as the router's fused dispatch kernel does. Returns this block's
+// {expert, first sorted row, rows, 0}, expert −1 past the call's distinct
+// experts. Every thread calls it; `lds` (fused_route_words(E) words of the
+// dynamic LDS) is free again on return. Requires E ≤ 256, k ≤ 16, J ≤ 16.
+__device__ int4 fused_route(const ExpertKArgs &p, int call, int32_t *lds) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int E = p.E, k = p.k, J = p.fr_J;
+  int32_t *ev = lds;                     // [16] distinct experts, ascending
+  int32_t *pv = lds + 16;                // [16] first sorted row of each
+  int32_t *cv = lds + 32;                // [16] rows of each
+  int32_t *nd = lds + 48;                // distinct count
+  float *rowbuf = (float *)(lds + 64);   // [2k] route row of the other blocks
+  int32_t *hist = lds + 96;              // [E]
+  int32_t *cur = hist + E;               // [E + 1]
+  const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+  if (threadIdx.x < WAVE) {
+    const float *part = p.fr_partial + (int64_t)call * J * E;
+    const float *b = p.fr_b ? p.fr_b + call * p.fr_b_cs : nullptr;
+    // Every chunk sum of the lane's experts loaded before the first add.
+    float v[4][16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = min(lane + WAVE * i, E - 1);
+#pragma unroll
+      for (int u = 0; u < 16; u++) v[i][u] = part[(int64_t)min(u, J - 1) * E + e];
+    }
+    float vals[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = lane + WAVE * i;
+      float sum = v[i][0];
+#pragma unroll
+      for (int u = 1; u < 16; u++)
+        if (u < J) sum = sum + v[i][u];
+      if (b && e < E) sum = sum + b[e];
+      vals[i] = e < E ? sum : -INFINITY;
+    }
+    // The route buffer is the layer's own (written here, read by the combine).
+    float *row = writer ? const_cast<float *>(p.route) + call * p.route_cs : rowbuf;
+    const int id = moe_dev::wave_topk_route<4>(vals, E, k, lane, row);
+    // The stable counting sort of the k slots: slot s goes to row
+    // (ids below its id) + (earlier slots with its id).
+    const int my = lane < k ? id : 0x7fffffff;
+    int less = 0, eqb = 0, cnt = 0;
+    for (int j = 0; j < k; j++) {
+      const int o = __shfl(my, j);
+      less += o < my;
+      eqb += (j < lane) && (o == my);
+      cnt += o == my;
+    }
+    const bool first = lane < k && eqb == 0;
+    int drank = 0;
+    for (int j = 0; j < k; j++) {
+      const int o = __shfl(my, j);
+      const int of = __shfl((int)first, j);
+      drank += of && o < my;
+    }
+    if (first) {
+      ev[drank] = my;
+      pv[drank] = less;
+      cv[drank] = cnt;
+    }
+    const int ndist = __popcll(__ballot(first));  // every lane votes: outside the branch
+    if (lane == 0) *nd = ndist;
+    if (writer) {
+      int32_t *perm = p.db.perm + call * p.db.perm_cs();
+      if (lane < k) perm[less + eqb] = lane;
+      for (int e = lane; e < E; e += WAVE) hist[e] = 0;
+      if (first) hist[my] = cnt;
+      moe_dev::wave_scan_experts(hist, E, p.fr_tile_m, lane, p.db.offsets + call * p.db.off_cs(),
+                                 p.db.tile_off + call * p.db.off_cs(),
+                                 p.db.active + call * p.db.act_cs(),
+                                 p.db.meta + call * p.db.meta_cs(), cur);
+    }
+  }
+  __syncthreads();
+  const int y = blockIdx.y;
+  int4 d = {-1, 0, 0, 0};
+  if (y < *nd) d = int4{ev[y], pv[y], cv[y], 0};
+  __syncthreads();
+  return d;
+}
 
 __device__ __forceinline__ float swiglu(float glu, float lin) {
   // activations.ts:127-133: g = min(glu, 7), l = clamp(lin, ±7),
@@ -195,7 +294,12 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
   _Float16 *ahi = (_Float16 *)smem;
 
   const int call = blockIdx.z;
-  const int4 desc = ((const int4 *)(p.db.active + call * p.db.act_cs()))[blockIdx.y];
+  int4 desc;
+  if (MODE == MODE_UP && p.fr_partial) {
+    desc = fused_route(p, call, (int32_t *)smem);
+  } else {
+    desc = ((const int4 *)(p.db.active + call * p.db.act_cs()))[blockIdx.y];
+  }
   const int e = desc.x;
   if (e < 0) return;
   const int p0 = desc.y, cnt = desc.z;
@@ -301,7 +405,8 @@ __global__ __launch_bounds__(64 * NWS * KS) __attribute__((amdgpu_waves_per_eu(N
       const int total = RC * cpr;
       const int srcv = lane >= rows ? 0
                        : (MODE == MODE_DOWN && p.sorted) ? p0 + c0 + lane
-                                                         : perm[p0 + c0 + lane] / p.a_row_div;
+                       : (MODE == MODE_UP && p.fr_partial) ? 0  // the call's one token
+                                                           : perm[p0 + c0 + lane] / p.a_row_div;
       const bool vec = p.K % EPC == 0 && (((uintptr_t)abase) & 15) == 0;
       const AT *nw = (const AT *)p.a_normw;
       const bool nvec = vec && (((uintptr_t)nw) & 15) == 0;
@@ -746,7 +851,8 @@ int launch_mode(const ExpertArgs &ea, const ExpertKArgs &p, hipStream_t s) {
     dim3 grid((ncg + cg_per_block - 1) / cg_per_block, max_active, ea.calls), block(64 * nw * ks);
     // Up parks one [4][64] floatx4 per stream (per pair when paired).
     const int parks = MODE == MODE_UP ? (ns == 1 ? nw / 2 : nw) : 0;
-    const size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, nw * (ks - 1));
+    size_t lds = skinny_lds_bytes(ea.K, split, q.rc, parks, nw * (ks - 1));
+    if (q.fr_partial) lds = std::max(lds, (size_t)fused_route_words(ea.E) * 4);
 #define SKINNY(AT_, GR_, NW_, NS_, KS_)                                                   \
   do {                                                                                    \
     if constexpr (MODE == MODE_UP) {                                                      \
@@ -801,9 +907,16 @@ bool expert_stages_norm(const ExpertArgs &ea) {
          (ea.g == ea.K || ea.g % 32 == 0);
 }
 
+bool expert_fuses_route(const ExpertArgs &up, int J) {
+  return expert_stages_norm(up) && up.A == up.k && up.a_row_div == up.k && up.E <= 256 &&
+         up.k <= 16 && J >= 1 && J <= 16;
+}
+
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   if (ea.a_normw && (!expert_stages_norm(ea) || !ea.a_inv))
     return moe_fail(MOE_EXECUTION_FAILED, "expert: the staged pre-norm needs the skinny gate/up kernel");
+  if (ea.mode == MODE_UP && ea.fr_partial && !expert_fuses_route(ea, ea.fr_J))
+    return moe_fail(MOE_EXECUTION_FAILED, "expert: the fused route needs a single-token call on the skinny gate/up kernel");
   MOE_NONNULL(ea.a);
   MOE_NONNULL(ea.route);
   MOE_NONNULL(ea.w0.w);
@@ -822,6 +935,11 @@ int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s) {
   if (expert_uses_gemm(ea)) return launch_expert_gemm(ea, db, s);
   ExpertKArgs p;
   p.sorted = ea.dispatch_order;
+  p.fr_partial = ea.mode == MODE_UP ? ea.fr_partial : nullptr;
+  p.fr_b = ea.fr_b;
+  p.fr_b_cs = ea.fr_b_cs;
+  p.fr_J = ea.fr_J;
+  p.fr_tile_m = ea.fr_tile_m;
   p.a = ea.a;
   p.a_cs = ea.a_cs;
   p.a_row_div = ea.a_row_div;

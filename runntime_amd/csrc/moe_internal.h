@@ -154,6 +154,9 @@ struct RouterArgs {
   const void *norm_w;
   float norm_eps;
   float *inv;
+  // Only the chunk sums (partial): the fold, top-k and dispatch run in the
+  // up product's prologue (ExpertArgs::fr_partial).
+  int chunks_only;
 };
 // Router + top-k. With T <= FUSED_T and `db` given, the dispatch of each call
 // is built in the same kernel and `dispatched` is set.
@@ -201,9 +204,24 @@ struct ExpertArgs {
   // a_normw [K] of x's dtype; NULL for plain x.
   const float *a_inv;
   const void *a_normw;
+  // Up of single-token calls on the skinny kernel (fr_partial non-NULL):
+  // the router's fold and top-k and the call's dispatch run in the kernel's
+  // prologue from the chunk sums fr_partial [J·E] per call (fr_J chunks) and
+  // the router bias fr_b (may be NULL; fr_b_cs per call); block (0, 0) of
+  // each call writes the route row (route) and the dispatch buffers that
+  // down and the combine read.
+  const float *fr_partial;
+  const float *fr_b;
+  int64_t fr_b_cs;
+  int fr_J;
+  int fr_tile_m;
 };
 
 int launch_expert(const ExpertArgs &ea, const DispatchBufs &db, hipStream_t s);
+// Whether the up product of these arguments can take the router's fold,
+// top-k and dispatch into its prologue (single-token calls on the skinny
+// kernel, E ≤ 256, J ≤ 16 chunks).
+bool expert_fuses_route(const ExpertArgs &up, int J);
 // The grouped GEMM (gemm.hip) for many rows per expert.
 bool gemm_eligible(const ExpertArgs &ea);
 // Whether launch_expert runs these arguments on the grouped GEMM.

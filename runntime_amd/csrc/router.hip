@@ -501,6 +501,10 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
     }
 #undef RC_LAUNCH
   }
+  if (ra.chunks_only) {
+    if (dispatched) *dispatched = true;
+    return 0;
+  }
   const int ni = (ra.E + WAVE - 1) / WAVE;
   // Fold batch: the chunk count J, rounded up to 8, 16 or 32 (8 with more
   // than two experts a lane).

@@ -398,6 +398,42 @@ def test_moe_layer_small_calls(T, d, E, k, I, x_dtype):
     assert_close(got_out, want_out, what="small call output")
 
 
+@pytest.mark.parametrize("d,E,k,x_dtype,calls", [(640, 128, 4, "f32", 1), (2048, 64, 8, "f16", 1),
+                                                  (640, 128, 4, "f32", 5), (200, 20, 16, "f16", 1),
+                                                  (1024, 256, 2, "f32", 3)])
+def test_single_token_route_is_the_routers(d, E, k, x_dtype, calls):
+    """A single single-token call takes the router's fold, top-k and
+    dispatch into the gate/up kernel's prologue; batched single-token calls
+    keep the router's own fold kernel. Either way the route row is the
+    standalone router's bit for bit (ids and gates), in every call, and the
+    output is the oracle's."""
+    import dataclasses
+    cfg = dataclasses.replace(CONFIGS[2], name="t1", T=1, d=d, E=E, k=k, I=384, x_dtype=x_dtype)
+    say(f"single-token route d={d} E={E} k={k} {x_dtype} calls={calls}")
+    from runntime_amd.synth import make_weight_copies
+    wc = make_weight_copies(cfg, calls, seed=51, device="cpu")
+    g = torch.Generator().manual_seed(52)
+    xdt = torch.float16 if x_dtype == "f16" else torch.float32
+    x = torch.randn((calls, 1, d), generator=g).to(xdt)
+    res = torch.randn((calls, 1, d), generator=g)
+    wc.router_b.copy_(torch.randn((calls, E), generator=g) * 0.1)
+    dev = lambda t: t.to(DEV)
+    dw = lambda w: QuantExpertWeight(QuantW(dev(w.w.words), w.w.dims), dev(w.scales), dev(w.bias))
+    out, route = rt.moe_layer_batched(dev(x), dev(wc.router_w), dev(wc.router_b), dw(wc.glu),
+                                      dw(wc.lin), dw(wc.down), dev(res), k)
+    out, route = host(out), host(route)
+    for c in range(calls):
+        want = host(rt.router_topk(dev(x[c]), dev(wc.router_w[c]), dev(wc.router_b[c]), k))
+        assert np.array_equal(route[c], want), f"call {c}: route differs from the router's"
+    xs = x[0].float().numpy()
+    wt = lambda w: (w.w.words[0].numpy().view(np.uint32), w.scales[0].numpy(), w.bias[0].numpy())
+    want_route = ref.topk(ref.router_logits(xs, wc.router_w[0].numpy(), wc.router_b[0].numpy()), k)
+    assert np.array_equal(route[0][:, :k], want_route[:, :k])
+    act = ref.moe_up(xs, want_route, wt(wc.glu), wt(wc.lin), 8, d, E)
+    want_out = ref.moe_down(act, want_route, wt(wc.down), res[0].numpy(), 8, cfg.I, E)
+    assert_close(out[0], want_out, what="single-token call 0")
+
+
 @pytest.mark.parametrize("T,E,k,x_dtype", [(64, 64, 16, "f32"), (17, 32, 8, "f16"),
                                            (64, 128, 4, "f32"), (65, 16, 4, "f32")])
 def test_moe_layer_fused_router_dispatch_limits(T, E, k, x_dtype):
