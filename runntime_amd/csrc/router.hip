@@ -372,31 +372,48 @@ __global__ __launch_bounds__(256) void k_router_chunks_tiled(RouterArgs ra) {
   // 8-element runs of a token's row (stored transposed), W as 4-expert runs.
   const bool vec = len == ROUTER_CHUNK && (d & 7) == 0 && (E & 3) == 0 && e0 + EB <= E;
   if (vec) {
+    // Every load of the tile before the first LDS store (a loop of load,
+    // store pairs waits one memory latency per iteration). A token past T
+    // reads token T − 1 and stores zeros.
     constexpr int XR = ROUTER_CHUNK / 8;  // runs per token row
-    for (int i = tid; i < TB * XR; i += 256) {
-      const int tt = i / XR, kk = (i % XR) * 8, t = t0 + tt;
-      float v[8];
-      if (t < Tn) {
-        if constexpr (sizeof(T) == 2) {
-          const half8v h = *(const half8v *)((const _Float16 *)x + (int64_t)t * d + k0 + kk);
+    constexpr int XN = TB * XR / 256, WN = ROUTER_CHUNK * EB / 4 / 256;
+    static_assert(TB * XR % 256 == 0 && ROUTER_CHUNK * EB / 4 % 256 == 0, "whole passes");
+    typedef float f8 __attribute__((ext_vector_type(8)));
+    f8 xv[XN];
+    float4 wv[WN];
 #pragma unroll
-          for (int q = 0; q < 8; q++) v[q] = (float)h[q];
-        } else {
-          const float4 a = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk);
-          const float4 b = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk + 4);
-          v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-          v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        }
+    for (int r = 0; r < XN; r++) {
+      const int i = tid + 256 * r;
+      const int tt = i / XR, kk = (i % XR) * 8, t = min(t0 + tt, Tn - 1);
+      if constexpr (sizeof(T) == 2) {
+        const half8v h = *(const half8v *)((const _Float16 *)x + (int64_t)t * d + k0 + kk);
+#pragma unroll
+        for (int q = 0; q < 8; q++) xv[r][q] = (float)h[q];
       } else {
-#pragma unroll
-        for (int q = 0; q < 8; q++) v[q] = 0.f;
+        const float4 a = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk);
+        const float4 b = *(const float4 *)((const float *)x + (int64_t)t * d + k0 + kk + 4);
+        xv[r] = f8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       }
-#pragma unroll
-      for (int q = 0; q < 8; q++) xs[(kk + q) * TB + tt] = v[q];
     }
-    for (int i = tid; i < ROUTER_CHUNK * EB / 4; i += 256) {
+#pragma unroll
+    for (int r = 0; r < WN; r++) {
+      const int i = tid + 256 * r;
       const int kk = i / (EB / 4), ee = (i % (EB / 4)) * 4;
-      *(float4 *)&ws[kk * EB + ee] = *(const float4 *)&w[(int64_t)(k0 + kk) * E + e0 + ee];
+      wv[r] = *(const float4 *)&w[(int64_t)(k0 + kk) * E + e0 + ee];
+    }
+#pragma unroll
+    for (int r = 0; r < XN; r++) {
+      const int i = tid + 256 * r;
+      const int tt = i / XR, kk = (i % XR) * 8;
+      const bool ok = t0 + tt < Tn;
+#pragma unroll
+      for (int q = 0; q < 8; q++) xs[(kk + q) * TB + tt] = ok ? xv[r][q] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < WN; r++) {
+      const int i = tid + 256 * r;
+      const int kk = i / (EB / 4), ee = (i % (EB / 4)) * 4;
+      *(float4 *)&ws[kk * EB + ee] = wv[r];
     }
   } else {
     for (int i = tid; i < ROUTER_CHUNK * TB; i += 256) {
