@@ -400,7 +400,8 @@ def test_moe_layer_small_calls(T, d, E, k, I, x_dtype):
 
 @pytest.mark.parametrize("d,E,k,x_dtype,calls", [(640, 128, 4, "f32", 1), (2048, 64, 8, "f16", 1),
                                                   (640, 128, 4, "f32", 5), (200, 20, 16, "f16", 1),
-                                                  (1024, 256, 2, "f32", 3)])
+                                                  (1024, 256, 2, "f32", 3), (64, 4, 1, "f32", 1),
+                                                  (132, 8, 8, "f32", 1), (1024, 256, 16, "f16", 1)])
 def test_single_token_route_is_the_routers(d, E, k, x_dtype, calls):
     """A single single-token call takes the router's fold, top-k and
     dispatch into the gate/up kernel's prologue; batched single-token calls
