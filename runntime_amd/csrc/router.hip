@@ -80,28 +80,31 @@ __device__ __forceinline__ void tile_rows_inv(const T *x, int64_t stride, int co
 
 // NORM: moe_block's pre-norm applied while staging (ra.norm_w); a template
 // flag, so that the plain instance keeps its few registers (occupancy).
+// EXB experts per block: 128, or fewer for launches with few blocks (a
+// single-token call has one block per chunk and expert tile: more, smaller
+// tiles spread its router weights over more CUs).
 // VEC (E a multiple of 4): W comes in 16-byte loads, four experts a lane.
 // One CU's load instructions, not bytes, bound this kernel: 4-byte loads
 // move ~23 GB/s per CU (256 B per wavefront instruction).
-template <typename T, bool NORM, bool VEC>
+template <typename T, bool NORM, bool VEC, int EXB>
 __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
   __shared__ float xs[RT_TOKENS * ROUTER_CHUNK];
-  __shared__ float ws[ROUTER_CHUNK * RT_EXPERTS];
+  __shared__ float ws[ROUTER_CHUNK * EXB];
   const int Tn = ra.T, d = ra.d, E = ra.E;
   const int J = (d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-  const int etiles = (E + RT_EXPERTS - 1) / RT_EXPERTS;
+  const int etiles = (E + EXB - 1) / EXB;
   const int call = blockIdx.z / etiles;
   const T *x = (const T *)ra.x + call * ra.x_cs;
   const float *w = ra.w + call * ra.w_cs;
   float *partial = ra.partial + call * ((int64_t)Tn * J * E);
   const int t0 = blockIdx.x * RT_TOKENS;
   const int j = blockIdx.y;
-  const int e0 = (blockIdx.z % etiles) * RT_EXPERTS;
-  const int et = min(RT_EXPERTS, E - e0);
+  const int e0 = (blockIdx.z % etiles) * EXB;
+  const int et = min(EXB, E - e0);
   const int k0 = j * ROUTER_CHUNK;
   const int len = min(ROUTER_CHUNK, d - k0);
   // Staging: every load of the tile is issued before the first LDS store.
-  constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * RT_EXPERTS / 256;
+  constexpr int XPER = RT_TOKENS * ROUTER_CHUNK / 256, WPER = ROUTER_CHUNK * EXB / 256;
   const T *nw = NORM ? (const T *)ra.norm_w : nullptr;
   float xv[XPER], nv[NORM ? XPER : 1];
   floatx4_r wv[WPER / 4];
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
 #pragma unroll
     for (int r = 0; r < WPER / 4; r++) {
       int i = threadIdx.x + 256 * r;
-      int kk = i / (RT_EXPERTS / 4), ee = 4 * (i % (RT_EXPERTS / 4));
+      int kk = i / (EXB / 4), ee = 4 * (i % (EXB / 4));
       wv[r] = (kk < len && ee < et)
                   ? __builtin_nontemporal_load((const floatx4_r *)(w + (int64_t)(k0 + kk) * E + e0 + ee))
                   : floatx4_r{0.f, 0.f, 0.f, 0.f};
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         int i = threadIdx.x + 256 * (4 * r + c);
-        int kk = i / RT_EXPERTS, ee = i % RT_EXPERTS;
+        int kk = i / EXB, ee = i % EXB;
         wv[r][c] = (kk < len && ee < et)
                        ? __builtin_nontemporal_load(w + (int64_t)(k0 + kk) * E + e0 + ee)
                        : 0.f;
@@ -180,14 +183,14 @@ __global__ __launch_bounds__(256) void k_router_chunks(RouterArgs ra) {
       for (int c = 0; c < 4; c++) ws[threadIdx.x + 256 * (4 * r + c)] = wv[r][c];
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < RT_TOKENS * RT_EXPERTS; p += blockDim.x) {
-    int tt = p / RT_EXPERTS, ee = p % RT_EXPERTS;
+  for (int p = threadIdx.x; p < RT_TOKENS * EXB; p += blockDim.x) {
+    int tt = p / EXB, ee = p % EXB;
     int t = t0 + tt;
     if (t >= Tn) break;
     if (ee >= et) continue;
     const float *xr = xs + tt * ROUTER_CHUNK;
     float c = 0.f;
-    for (int kk = 0; kk < len; kk++) c = fmaf(xr[kk], ws[kk * RT_EXPERTS + ee], c);
+    for (int kk = 0; kk < len; kk++) c = fmaf(xr[kk], ws[kk * EXB + ee], c);
     partial[((int64_t)t * J + j) * E + e0 + ee] = c;
   }
 }
@@ -502,14 +505,23 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
     }
   } else {
     const int J = (ra.d + ROUTER_CHUNK - 1) / ROUTER_CHUNK;
-    const int etiles = (ra.E + RT_EXPERTS - 1) / RT_EXPERTS;
+    // Expert tiles of 128, or 64 / 32 while the launch has under 256 blocks.
+    const long tt = ((long)ra.T + RT_TOKENS - 1) / RT_TOKENS * J * ra.calls;
+    const int exb = tt * ((ra.E + 127) / 128) >= 256 ? 128 : tt * ((ra.E + 63) / 64) >= 256 ? 64 : 32;
+    const int etiles = (ra.E + exb - 1) / exb;
     dim3 grid((ra.T + RT_TOKENS - 1) / RT_TOKENS, J, etiles * ra.calls), block(256);
     // 16-byte W loads need every row of W 16-byte aligned.
     const bool vec = ra.E % 4 == 0 && ((uintptr_t)ra.w & 15) == 0 && ra.w_cs % 4 == 0;
-#define RC_LAUNCH(T_, N_)                                                                      \
-  do {                                                                                         \
-    if (vec) hipLaunchKernelGGL((k_router_chunks<T_, N_, true>), grid, block, 0, s, ra);       \
-    else hipLaunchKernelGGL((k_router_chunks<T_, N_, false>), grid, block, 0, s, ra);          \
+#define RC_EXB(T_, N_, V_)                                                                       \
+  do {                                                                                           \
+    if (exb == 128) hipLaunchKernelGGL((k_router_chunks<T_, N_, V_, 128>), grid, block, 0, s, ra); \
+    else if (exb == 64) hipLaunchKernelGGL((k_router_chunks<T_, N_, V_, 64>), grid, block, 0, s, ra); \
+    else hipLaunchKernelGGL((k_router_chunks<T_, N_, V_, 32>), grid, block, 0, s, ra);           \
+  } while (0)
+#define RC_LAUNCH(T_, N_)                 \
+  do {                                    \
+    if (vec) RC_EXB(T_, N_, true);        \
+    else RC_EXB(T_, N_, false);           \
   } while (0)
     if (ra.x_dtype == MOE_F16) {
       if (ra.norm_w) RC_LAUNCH(_Float16, true); else RC_LAUNCH(_Float16, false);
@@ -517,6 +529,7 @@ int launch_router_topk(const RouterArgs &ra, const DispatchBufs *db, int tile_m,
       if (ra.norm_w) RC_LAUNCH(float, true); else RC_LAUNCH(float, false);
     }
 #undef RC_LAUNCH
+#undef RC_EXB
   }
   if (ra.chunks_only) {
     if (dispatched) *dispatched = true;
